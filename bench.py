@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention engine on one MI355X.
+
+Workload (the metric's configuration): full 24-layer Qwen2-0.5B-shape decode attention for one
+token, batch 1, 14 query / 2 KV heads, head_dim 64, 4096 cached tokens, K cache q8_0 and V cache
+q4_0 produced by ggml's reference quantizers (cvattn_set_rows, bit-exact to quantize_row_*_ref)
+from seeded N(0,1) values, N(0,1) queries, scale 1/8.
+
+A step is one token's attention over all 24 layers.  The timed step runs the 24 layer problems
+as one prepared batch (cvattn_fa_batch_launch: one kernel, split partials merged in-kernel);
+R independent copies of the 24-layer cache (R * 20.6 MB >= 512 MB) are cycled so every step
+streams its KV bytes from HBM, not from the 256 MB Infinity Cache.  The R launches are captured
+in one HIP graph and replayed.  Reported alongside, measured in the same run:
+  * the real decode cadence (24 dependent per-layer launches per token),
+  * flow-DiT attention (T=1500, batch 2 for CFG, 16 heads, fp16) TFLOP/s,
+  * the CPU baseline: the ggml CPU flash-attention loop restated in oracle/ (a port), timed on a
+    bounded sample of the same decode workload on the host cores.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+sys.path.insert(0, os.path.join(ROOT, "cosyvoice.cpp_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+FP16_DENSE_PEAK_TFLOPS = 2500.0  # MI355X dense fp16 MFMA
+
+L, H, HKV, D, NKV, MAX_SEQ = 24, 14, 2, 64, 4096, 4096
+KT_NAME, VT_NAME = "q8_0", "q4_0"
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def decode_bytes_per_layer(kt_bytes, vt_bytes, n_kv=NKV):
+    # n_kv * H_kv * (D/32) * (bK + bV) + Q + O (f32)
+    return n_kv * HKV * (D // 32) * (kt_bytes + vt_bytes) + 2 * H * D * 4
+
+
+def build_decode(lib, cvattn, torch, dev, n_copies, kt, vt):
+    """R copies x 24 layers of K/V caches quantized on the device, plus Q and outputs."""
+    rk = cvattn.row_bytes(kt, HKV * D)
+    rv = cvattn.row_bytes(vt, HKV * D)
+    kbuf = torch.empty((n_copies, L, MAX_SEQ, rk), dtype=torch.uint8, device=dev)
+    vbuf = torch.empty((n_copies, L, MAX_SEQ, rv), dtype=torch.uint8, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20261201)
+    idx = torch.arange(MAX_SEQ, dtype=torch.int32, device=dev)
+    it = cvattn.contiguous(idx.data_ptr(), cvattn.I32, [MAX_SEQ, 1, 1, 1])
+    src = torch.empty((MAX_SEQ, HKV * D), dtype=torch.float32, device=dev)
+    st = cvattn.contiguous(src.data_ptr(), cvattn.F32, [HKV * D, MAX_SEQ, 1, 1])
+    for r in range(n_copies):
+        for layer in range(L):
+            for buf, t in ((kbuf, kt), (vbuf, vt)):
+                src.normal_(generator=gen)
+                dt = cvattn.contiguous(buf[r, layer].data_ptr(), t, [HKV * D, MAX_SEQ, 1, 1])
+                rc = lib.set_rows(dt, st, it)
+                assert rc == cvattn.OK, lib.status_string(rc)
+    q = torch.randn((n_copies, L, H, D), generator=gen, device=dev, dtype=torch.float32)
+    out = torch.zeros((n_copies, L, H, D), dtype=torch.float32, device=dev)
+    torch.cuda.synchronize()
+
+    def problem(r, layer):
+        p = cvattn.FaProblem()
+        p.q = cvattn.llm_q_view(q[r, layer].data_ptr(), D, H, 1)
+        p.k = cvattn.llm_kv_view(kbuf[r, layer].data_ptr(), kt, D, HKV, NKV, MAX_SEQ)
+        p.v = cvattn.llm_kv_view(vbuf[r, layer].data_ptr(), vt, D, HKV, NKV, MAX_SEQ)
+        p.dst = cvattn.out_view(out[r, layer].data_ptr(), D, H, 1)
+        return p
+
+    return kbuf, vbuf, q, out, problem
+
+
+def make_plan(lib, cvattn, torch, dev, probs, keep):
+    wsb = lib.fa_batch_workspace(probs)
+    assert wsb > 0, "batch rejected"
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    keep.append(ws)
+    rc, plan = lib.fa_batch_prepare(probs, 1.0 / math.sqrt(D), ws.data_ptr(), ws.numel(),
+                                    torch.cuda.current_stream().cuda_stream)
+    assert rc == cvattn.OK, lib.status_string(rc)
+    keep.append(plan)
+    return plan
+
+
+def time_graph(torch, launch_fn, n_per_graph, steps, warmup):
+    """Capture launch_fn (n_per_graph steps) in a HIP graph; return ms per step over `steps`."""
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        launch_fn(stream.cuda_stream)  # eager warm-up of the code path
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        launch_fn(stream.cuda_stream)
+    torch.cuda.synchronize()
+    reps_w = max(1, math.ceil(warmup / n_per_graph))
+    reps = max(1, steps // n_per_graph)
+    for _ in range(reps_w):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    start.record(cur)
+    for _ in range(reps):
+        graph.replay()
+    end.record(cur)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / (reps * n_per_graph), reps * n_per_graph
+
+
+def bench_dit(lib, cvattn, torch, dev, iters=50):
+    """Flow-DiT attention layer call: T=1500, B=2, 16 heads, fp16 q/k/v views, no mask."""
+    T, B, HD = 1500, 2, 16
+    q = torch.randn((B, T, HD * D), device=dev, dtype=torch.float16)
+    k = torch.randn((B, T, HD * D), device=dev, dtype=torch.float16)
+    v = torch.randn((B, T, HD * D), device=dev, dtype=torch.float16)
+    out = torch.empty((B, T, HD, D), device=dev, dtype=torch.float32)
+    p = cvattn.FaProblem()
+    p.q = cvattn.dit_view(q.data_ptr(), T, B, ttype=cvattn.F16)
+    p.k = cvattn.dit_view(k.data_ptr(), T, B, ttype=cvattn.F16)
+    p.v = cvattn.dit_view(v.data_ptr(), T, B, ttype=cvattn.F16)
+    p.dst = cvattn.out_view(out.data_ptr(), D, HD, T, B)
+    keep = []
+    plan = make_plan(lib, cvattn, torch, dev, [p], keep)
+
+    def launch(s):
+        for _ in range(10):
+            assert lib.fa_batch_launch(plan, s) == cvattn.OK
+
+    ms, n = time_graph(torch, launch, 10, iters, 10)
+    flops = 4.0 * D * B * HD * T * T
+    return {"ms_per_layer_call": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flop_per_call": flops, "calls": n}
+
+
+def cpu_baseline(kbuf, vbuf, q, budget_s=12.0):
+    """ggml CPU flash-attention loop (restated in oracle/) on copy 0 of the decode workload."""
+    import numpy as np
+
+    from oracle.oracle import Q4_0, Q8_0, oracle, row_bytes, view
+
+    orc = oracle()
+    threads = min(H, len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count())
+    rk, rv = row_bytes(Q8_0, HKV * D), row_bytes(Q4_0, HKV * D)
+    kh = kbuf[0].cpu().numpy()
+    vh = vbuf[0].cpu().numpy()
+    qh = q[0].cpu().numpy()
+    layers_done, t0 = 0, time.perf_counter()
+    while True:
+        layer = layers_done % L
+        qt = view(qh[layer], 0, [D, 1, H, 1], [4, 4 * D * H, 4 * D, 4 * D * H])
+        kt = view(kh[layer], Q8_0, [D, NKV, HKV, 1], [34, rk, rk // HKV, rk * MAX_SEQ])
+        vt = view(vh[layer], Q4_0, [D, NKV, HKV, 1], [18, rv, rv // HKV, rv * MAX_SEQ])
+        orc.fa_ggml_cpu(qt, kt, vt, None, 0.125, (H, D), n_threads=threads)
+        layers_done += 1
+        el = time.perf_counter() - t0
+        if layers_done % L == 0 and el >= budget_s:
+            break
+        if layers_done >= 50 * L:
+            break
+    sec_per_token = el / (layers_done / L)
+    gbs = decode_bytes_per_layer(34, 18) * L / sec_per_token / 1e9
+    return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "tok_per_s": 1.0 / sec_per_token,
+            "sample": f"{layers_done // L} tokens x 24 layers of the same q8_0/q4_0 4096-token decode, "
+                      f"ggml CPU flash-attention loop restated in C (oracle/oracle.c), {threads} threads"}
+
+
+def read_traffic():
+    """HBM bytes per launch of the decode kernel from the committed rocprofv3 counter summary."""
+    path = os.path.join(ROOT, "profiles", "decode_q8_0_q4_0_24x4096_counters.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1])
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2600)
+    ap.add_argument("--warmup", type=int, default=260)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-dit", action="store_true", help="skip the DiT leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this attention path has "
+              "no multi-GPU form here: see DESIGN.md for how it would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import cvattn
+
+    lib = cvattn.lib()
+    dev = torch.device("cuda:0")
+    kt, vt = cvattn.Q8_0, cvattn.Q4_0
+    per_layer = decode_bytes_per_layer(34, 18)
+    per_copy = L * (MAX_SEQ * (cvattn.row_bytes(kt, HKV * D) + cvattn.row_bytes(vt, HKV * D)))
+    n_copies = max(2, math.ceil(512 * 2**20 / per_copy))
+    log(f"building {n_copies} copies of the 24-layer q8_0/q4_0 cache ({n_copies * per_copy / 2**20:.0f} MiB)")
+    kbuf, vbuf, q, out, problem = build_decode(lib, cvattn, torch, dev, n_copies, kt, vt)
+
+    keep = []
+    plans = [make_plan(lib, cvattn, torch, dev, [problem(r, l) for l in range(L)], keep) for r in range(n_copies)]
+
+    def launch_batched(s):
+        for p in plans:
+            assert lib.fa_batch_launch(p, s) == cvattn.OK
+
+    steps = max(n_copies, (args.steps // n_copies) * n_copies)
+    ms, steps_done = time_graph(torch, launch_batched, n_copies, steps, args.warmup)
+    bytes_step = per_layer * L
+    gbs = bytes_step / (ms * 1e-3) / 1e9
+    log(f"decode 24x4096 batched: {ms * 1e3:.2f} us/token, {gbs:.0f} GB/s")
+
+    # real decode cadence: 24 dependent per-layer launches per token
+    layer_plans = [[make_plan(lib, cvattn, torch, dev, [problem(r, l)], keep) for l in range(L)]
+                   for r in range(n_copies)]
+
+    def launch_layers(s):
+        for r in range(n_copies):
+            for p in layer_plans[r]:
+                assert lib.fa_batch_launch(p, s) == cvattn.OK
+
+    ms_seq, _ = time_graph(torch, launch_layers, n_copies, max(n_copies, steps // 4), n_copies)
+    log(f"decode 24 sequential layer launches: {ms_seq * 1e3:.2f} us/token")
+
+    dit = None if args.no_dit else bench_dit(lib, cvattn, torch, dev)
+    if dit:
+        log(f"dit T=1500: {dit['ms_per_layer_call'] * 1e3:.1f} us/call, {dit['tflops']:.1f} TFLOP/s")
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(kbuf, vbuf, q)
+        log(f"cpu baseline: {cpu['value']:.3f} GB/s ({cpu['cores']} threads)")
+
+    traffic = read_traffic()
+    res = {
+        "metric": "LLM decode-attn GB/s + tok/s (q8_0 KV, 4k ctx); DiT attn TFLOP/s",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps_done,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q8_0/q4_0 KV, f16 MFMA, f32 accumulate",
+        "data": "synthetic: seeded N(0,1) K/V quantized on device with ggml's reference quantizers, N(0,1) Q",
+        "config": {
+            "workload": "decode attention, 24 layers x 1 token, batch 1, 14/2 heads, head_dim 64, "
+                        "kv_len 4096, K q8_0 / V q4_0 (the 24 layers run as one prepared batch)",
+            "kv_copies_cycled": n_copies,
+            "bytes_per_step": bytes_step,
+        },
+        "tok_per_s": 1000.0 / ms,
+        "tok_per_s_layer_sequential": 1000.0 / ms_seq,
+        "us_per_token_layer_sequential": ms_seq * 1e3,
+        "dit_attn": None if dit is None else {
+            "workload": "flow-DiT attention layer call, T=1500, batch 2, 16 heads, head_dim 64, fp16, no mask",
+            "tflops": dit["tflops"], "ms_per_layer_call": dit["ms_per_layer_call"],
+            "mfma_frac": dit["tflops"] / FP16_DENSE_PEAK_TFLOPS,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": gbs / HBM_PEAK_GBS,
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,435 @@
+// cvattn_api.cpp -- the C ABI of include/cvattn.h: argument validation (the shape rules of
+// ggml_flash_attn_ext / ggml_set_rows as cosyvoice.cpp uses them), workspace planning and
+// dispatch to the gfx950 kernels.  No device allocation, no host<->device synchronisation.
+#include "../../include/cvattn.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "cvattn_common.h"
+#include "cvattn_launch.h"
+
+using namespace cvattn;
+
+namespace {
+
+constexpr int kTargetUnits = 512;  // ~2 workgroups per CU on a 256-CU MI355X
+constexpr size_t kAlign = 256;
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+bool is_kv_type(int t) {
+    return t == T_F32 || t == T_F16 || t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_1 || t == T_Q5_0 || t == T_Q5_1;
+}
+
+// A head row of the K/V view must be contiguous: nb0 equals the element/block size.
+bool kv_ok(const cvattn_tensor *t) {
+    if (!t || !t->data || !is_kv_type(t->type)) return false;
+    if (t->ne[0] != HEAD) return false;
+    if (t->nb[0] != (size_t)type_bytes(t->type)) return false;
+    for (int i = 1; i < 4; i++)
+        if (t->ne[i] <= 0 && !(i == 1 && t->ne[1] == 0)) return false;
+    return true;
+}
+
+struct FaShape {
+    int n_q, H, H_kv, G, B, n_kv;
+    int n_rows, n_rowgroups;
+    FaKernelShape ks;
+};
+
+int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
+             const cvattn_tensor *mask, FaShape *sh) {
+    if (!q || !k || !v) return CVATTN_ERR_BAD_ARGS;
+    if (!q->data) return CVATTN_ERR_BAD_ARGS;
+    if (q->type != T_F32 && q->type != T_F16) return CVATTN_ERR_UNSUPPORTED;
+    if (q->ne[0] != HEAD || k->ne[0] != HEAD || v->ne[0] != HEAD) return CVATTN_ERR_UNSUPPORTED;
+    if (q->nb[0] != (size_t)type_bytes(q->type)) return CVATTN_ERR_UNSUPPORTED;
+    if (!kv_ok(k) || !kv_ok(v)) return is_kv_type(k->type) && is_kv_type(v->type) ? CVATTN_ERR_BAD_ARGS : CVATTN_ERR_UNSUPPORTED;
+    for (int i = 1; i < 4; i++)
+        if (q->ne[i] <= 0) return CVATTN_ERR_BAD_ARGS;
+    if (k->ne[1] != v->ne[1]) return CVATTN_ERR_BAD_ARGS;
+    if (k->ne[2] != v->ne[2]) return CVATTN_ERR_UNSUPPORTED;
+    if (q->ne[2] % k->ne[2]) return CVATTN_ERR_BAD_ARGS;
+    if (q->ne[3] % k->ne[3] || q->ne[3] % v->ne[3]) return CVATTN_ERR_BAD_ARGS;
+    if (mask && mask->data) {
+        if (mask->type != T_F16 || mask->nb[0] != 2) return CVATTN_ERR_UNSUPPORTED;
+        if (mask->ne[0] < k->ne[1] || mask->ne[1] < q->ne[1]) return CVATTN_ERR_BAD_ARGS;
+        if (mask->ne[2] <= 0 || mask->ne[3] <= 0) return CVATTN_ERR_BAD_ARGS;
+        if (q->ne[2] % mask->ne[2] || q->ne[3] % mask->ne[3]) return CVATTN_ERR_BAD_ARGS;
+    }
+    const int64_t lim = (int64_t)1 << 30;
+    if (q->ne[1] >= lim || q->ne[2] >= lim || q->ne[3] >= lim || k->ne[1] >= lim) return CVATTN_ERR_UNSUPPORTED;
+    sh->n_q = (int)q->ne[1];
+    sh->H = (int)q->ne[2];
+    sh->H_kv = (int)k->ne[2];
+    sh->G = sh->H / sh->H_kv;
+    sh->B = (int)q->ne[3];
+    sh->n_kv = (int)k->ne[1];
+    sh->n_rows = sh->n_q * sh->G;
+    sh->ks = fa_shape(sh->n_rows);
+    sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
+    return CVATTN_OK;
+}
+
+int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
+    if (!dst || !dst->data) return CVATTN_ERR_BAD_ARGS;
+    if (dst->type != T_F32) return CVATTN_ERR_UNSUPPORTED;
+    const int64_t want[4] = {HEAD, sh.H, sh.n_q, sh.B};
+    size_t stride = 4;
+    for (int i = 0; i < 4; i++) {
+        if (dst->ne[i] != want[i]) return CVATTN_ERR_BAD_ARGS;
+        if (dst->nb[i] != stride) return CVATTN_ERR_BAD_ARGS;
+        stride *= (size_t)want[i];
+    }
+    return CVATTN_OK;
+}
+
+// Token splits.  Decode-shaped problems (waves split the tokens) size each wave's token run so
+// the whole launch has ~kTargetWaves waves in flight; row-tiled problems split only when their
+// row groups alone cannot fill the chip.  `work` is the launch-wide sum of
+// B*H_kv*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
+constexpr int64_t kTargetWaves = 2048;
+
+void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
+    const int tstep = sh.ks.tstep;
+    int len;
+    if (sh.ks.wsplit) {
+        int64_t wlen = (std::max<int64_t>(1, work) + kTargetWaves - 1) / kTargetWaves;
+        wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
+        len = (int)wlen * sh.ks.nw;
+    } else {
+        const int min_split = 256;
+        const int64_t base = std::max<int64_t>(1, work);
+        int want = (int)std::max<int64_t>(1, (kTargetUnits + base - 1) / base);
+        want = std::min(want, std::max(1, (n_kv + min_split - 1) / min_split));
+        len = (n_kv + want - 1) / want;
+        len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
+    }
+    *split_len = len;
+    *n_splits = n_kv > 0 ? (n_kv + len - 1) / len : 1;
+}
+
+int64_t split_work(const FaShape &sh) {
+    const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
+    return sh.ks.wsplit ? groups * sh.n_kv : groups;
+}
+
+void fill_problem(FaProblem &p, const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
+                  const cvattn_tensor *mask, const cvattn_tensor *dst, const FaShape &sh) {
+    std::memset(&p, 0, sizeof(p));
+    p.q = q->data;
+    p.k = k->data;
+    p.v = v->data;
+    p.dst = (float *)dst->data;
+    p.q_nb1 = (int64_t)q->nb[1];
+    p.q_nb2 = (int64_t)q->nb[2];
+    p.q_nb3 = (int64_t)q->nb[3];
+    p.k_nb1 = (int64_t)k->nb[1];
+    p.k_nb2 = (int64_t)k->nb[2];
+    p.k_nb3 = (int64_t)k->nb[3];
+    p.v_nb1 = (int64_t)v->nb[1];
+    p.v_nb2 = (int64_t)v->nb[2];
+    p.v_nb3 = (int64_t)v->nb[3];
+    if (mask && mask->data) {
+        p.mask = mask->data;
+        p.m_nb1 = (int64_t)mask->nb[1];
+        p.m_nb2 = (int64_t)mask->nb[2];
+        p.m_nb3 = (int64_t)mask->nb[3];
+        p.m_ne2 = (int32_t)mask->ne[2];
+        p.m_ne3 = (int32_t)mask->ne[3];
+    } else {
+        p.m_ne2 = 1;
+        p.m_ne3 = 1;
+    }
+    p.n_kv = sh.n_kv;
+    p.rk3 = (int32_t)(sh.B / k->ne[3]);
+    p.rv3 = (int32_t)(sh.B / v->ne[3]);
+}
+
+void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
+    std::memset(&u, 0, sizeof(u));
+    u.n_q = sh.n_q;
+    u.H = sh.H;
+    u.H_kv = sh.H_kv;
+    u.G = sh.G;
+    u.B = sh.B;
+    u.n_rows = sh.n_rows;
+    u.n_rowgroups = sh.n_rowgroups;
+    u.q_f16 = q_type == T_F16 ? 1 : 0;
+    u.scale_log2 = scale * 1.4426950408889634f;
+}
+
+int64_t slots_per_split(const FaShape &sh) {
+    return (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * sh.ks.rows_per_group;
+}
+
+// Plan for a single problem: splits and the workspace size.
+struct SinglePlan {
+    FaShape sh;
+    int n_splits, split_len;
+    size_t ws_bytes;
+};
+
+int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
+                const cvattn_tensor *mask, SinglePlan *pl) {
+    int rc = check_fa(q, k, v, mask, &pl->sh);
+    if (rc) return rc;
+    const FaShape &sh = pl->sh;
+    plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len);
+    pl->ws_bytes = pl->n_splits > 1 ? (size_t)slots_per_split(sh) * pl->n_splits * PART_STRIDE * sizeof(float) : 0;
+    return CVATTN_OK;
+}
+
+// Host-side launch plan for batches (stored in cvattn_fa_plan::opaque).
+struct BatchPlan {
+    uint32_t magic;
+    int32_t ktype, vtype, has_mask;
+    FaKernelShape ks;
+    FaArgs args;
+};
+static_assert(sizeof(BatchPlan) <= sizeof(cvattn_fa_plan), "plan too large");
+constexpr uint32_t kPlanMagic = 0x43564150u;
+
+int hip_status(hipError_t e) { return e == hipSuccess ? CVATTN_OK : CVATTN_ERR_HIP; }
+
+} // namespace
+
+extern "C" {
+
+CVATTN_API int cvattn_supports_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
+                                              const cvattn_tensor *v, const cvattn_tensor *mask) {
+    FaShape sh;
+    return check_fa(q, k, v, mask, &sh) == CVATTN_OK ? 1 : 0;
+}
+
+CVATTN_API size_t cvattn_flash_attn_ext_workspace(const cvattn_tensor *q, const cvattn_tensor *k,
+                                                  const cvattn_tensor *v, const cvattn_tensor *mask) {
+    SinglePlan pl;
+    if (plan_single(q, k, v, mask, &pl)) return 0;
+    return pl.ws_bytes;
+}
+
+CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
+                                     const cvattn_tensor *v, const cvattn_tensor *mask,
+                                     const cvattn_tensor *dst, float scale, float max_bias,
+                                     float logit_softcap, int prec, void *ws, size_t ws_bytes,
+                                     cvattn_stream_t stream) {
+    if (max_bias != 0.0f || logit_softcap != 0.0f) return CVATTN_ERR_UNSUPPORTED;
+    if (prec != CVATTN_PREC_DEFAULT && prec != CVATTN_PREC_F32) return CVATTN_ERR_BAD_ARGS;
+    if (!std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
+    SinglePlan pl;
+    int rc = plan_single(q, k, v, mask, &pl);
+    if (rc) return rc;
+    rc = check_dst(dst, pl.sh);
+    if (rc) return rc;
+    if (ws_bytes < pl.ws_bytes || (pl.ws_bytes && !ws)) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
+    FaArgs a;
+    std::memset(&a, 0, sizeof(a));
+    fill_uniform(a.u, pl.sh, q->type, scale);
+    fill_problem(a.p0, q, k, v, mask, dst, pl.sh);
+    a.p0.n_splits = pl.n_splits;
+    a.p0.split_len = pl.split_len;
+    a.u.n_problems = 1;
+    a.u.total_units = (int64_t)pl.sh.B * pl.sh.H_kv * pl.sh.n_rowgroups * pl.n_splits;
+    a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
+    a.u.partials = (float *)ws;
+    const bool has_mask = mask && mask->data;
+    return hip_status(fa_launch(pl.sh.ks, k->type, v->type, has_mask, false, a, (hipStream_t)stream));
+}
+
+// ---- batches ------------------------------------------------------------------------------
+
+// Workspace of a prepared batch: [problem table | split-arrival counters | split partials].
+struct BatchLayout {
+    size_t table_bytes, counter_bytes, total_bytes;
+    int64_t units, rows;
+};
+
+static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProblem> *table, FaShape *sh0,
+                      BatchLayout *lay) {
+    if (!probs || n <= 0) return CVATTN_ERR_BAD_ARGS;
+    const bool has_mask = probs[0].mask.data != nullptr;
+    int rc = check_fa(&probs[0].q, &probs[0].k, &probs[0].v, has_mask ? &probs[0].mask : nullptr, sh0);
+    if (rc) return rc;
+    int64_t work = 0;
+    for (int i = 0; i < n; i++) {
+        const cvattn_fa_problem &p = probs[i];
+        FaShape sh;
+        if ((p.mask.data != nullptr) != has_mask) return CVATTN_ERR_BAD_ARGS;
+        rc = check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
+        if (rc) return rc;
+        rc = check_dst(&p.dst, sh);
+        if (rc) return rc;
+        if (p.q.type != probs[0].q.type || p.k.type != probs[0].k.type || p.v.type != probs[0].v.type)
+            return CVATTN_ERR_BAD_ARGS;
+        if (sh.n_q != sh0->n_q || sh.H != sh0->H || sh.H_kv != sh0->H_kv || sh.B != sh0->B) return CVATTN_ERR_BAD_ARGS;
+        work += split_work(sh);
+    }
+    if (table) table->resize(n);
+    int64_t unit = 0, part = 0, row = 0, cnt = 0;
+    for (int i = 0; i < n; i++) {
+        const cvattn_fa_problem &p = probs[i];
+        FaShape sh;
+        check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
+        int ns, sl;
+        plan_splits(sh, sh.n_kv, work, &ns, &sl);
+        FaProblem fp;
+        fill_problem(fp, &p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &p.dst, sh);
+        fp.n_splits = ns;
+        fp.split_len = sl;
+        fp.unit_begin = unit;
+        fp.part_begin = part;
+        fp.row_begin = row;
+        fp.cnt_begin = cnt;
+        const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
+        unit += groups * ns;
+        if (ns > 1) {
+            part += slots_per_split(sh) * ns;
+            cnt += groups;
+        }
+        row += (int64_t)sh.B * sh.H * sh.n_q;
+        if (table) (*table)[i] = fp;
+    }
+    lay->table_bytes = align_up(sizeof(FaProblem) * (size_t)n, kAlign);
+    lay->counter_bytes = align_up(sizeof(uint32_t) * (size_t)cnt, kAlign);
+    lay->total_bytes = lay->table_bytes + lay->counter_bytes + (size_t)part * PART_STRIDE * sizeof(float);
+    lay->units = unit;
+    lay->rows = row;
+    return CVATTN_OK;
+}
+
+CVATTN_API size_t cvattn_fa_batch_workspace(const cvattn_fa_problem *problems, int n) {
+    FaShape sh;
+    BatchLayout lay;
+    if (plan_batch(problems, n, nullptr, &sh, &lay)) return 0;
+    return lay.total_bytes;
+}
+
+CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n, float scale,
+                                       void *ws, size_t ws_bytes, cvattn_stream_t stream,
+                                       cvattn_fa_plan *plan) {
+    if (!plan || !std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
+    std::vector<FaProblem> table;
+    FaShape sh;
+    BatchLayout lay;
+    int rc = plan_batch(problems, n, &table, &sh, &lay);
+    if (rc) return rc;
+    if (!ws || ws_bytes < lay.total_bytes) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
+    BatchPlan bp;
+    std::memset(&bp, 0, sizeof(bp));
+    bp.magic = kPlanMagic;
+    bp.ks = sh.ks;
+    bp.ktype = problems[0].k.type;
+    bp.vtype = problems[0].v.type;
+    bp.has_mask = problems[0].mask.data != nullptr;
+    fill_uniform(bp.args.u, sh, problems[0].q.type, scale);
+    bp.args.u.n_problems = n;
+    bp.args.u.total_units = lay.units;
+    bp.args.u.total_rows = lay.rows;
+    bp.args.u.counters = (uint32_t *)((char *)ws + lay.table_bytes);
+    bp.args.u.partials = (float *)((char *)ws + lay.table_bytes + lay.counter_bytes);
+    bp.args.p0 = table[0];
+    bp.args.table = (const FaProblem *)ws;
+    // one upload: the table followed by zeroed counters (the kernels keep them zero afterwards)
+    std::vector<unsigned char> head(lay.table_bytes + lay.counter_bytes, 0);
+    std::memcpy(head.data(), table.data(), sizeof(FaProblem) * (size_t)n);
+    hipError_t e = hipMemcpyAsync(ws, head.data(), head.size(), hipMemcpyHostToDevice, (hipStream_t)stream);
+    if (e == hipSuccess) e = hipStreamSynchronize((hipStream_t)stream); // `head` must outlive the copy
+    if (e != hipSuccess) return CVATTN_ERR_HIP;
+    std::memset(plan, 0, sizeof(*plan));
+    std::memcpy(plan, &bp, sizeof(bp));
+    return CVATTN_OK;
+}
+
+CVATTN_API int cvattn_fa_batch_launch(const cvattn_fa_plan *plan, cvattn_stream_t stream) {
+    if (!plan) return CVATTN_ERR_BAD_ARGS;
+    BatchPlan bp;
+    std::memcpy(&bp, plan, sizeof(bp));
+    if (bp.magic != kPlanMagic) return CVATTN_ERR_BAD_ARGS;
+    return hip_status(fa_launch(bp.ks, bp.ktype, bp.vtype, bp.has_mask != 0, true, bp.args, (hipStream_t)stream));
+}
+
+// ---- formats ------------------------------------------------------------------------------
+
+CVATTN_API int64_t cvattn_block_size(int type) { return is_kv_type(type) ? type_block(type) : 0; }
+CVATTN_API int64_t cvattn_type_size(int type) { return is_kv_type(type) ? type_bytes(type) : 0; }
+
+CVATTN_API int cvattn_dequantize(int type, const void *src, float *dst, int64_t n, cvattn_stream_t stream) {
+    if (!is_kv_type(type)) return CVATTN_ERR_UNSUPPORTED;
+    if (n < 0 || (n > 0 && (!src || !dst))) return CVATTN_ERR_BAD_ARGS;
+    if (n % type_block(type)) return CVATTN_ERR_BAD_ARGS;
+    return hip_status(dequant_launch(type, src, dst, n, (hipStream_t)stream));
+}
+
+// ---- KV write ------------------------------------------------------------------------------
+
+static int check_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src, const cvattn_tensor *idx) {
+    if (!dst || !src || !idx) return CVATTN_ERR_BAD_ARGS;
+    if (!is_kv_type(dst->type)) return CVATTN_ERR_UNSUPPORTED;
+    if (src->type != T_F32 || src->nb[0] != 4) return CVATTN_ERR_UNSUPPORTED;
+    if (idx->type != T_I32 && idx->type != 27 /* GGML_TYPE_I64 */) return CVATTN_ERR_UNSUPPORTED;
+    if (dst->nb[0] != (size_t)type_bytes(dst->type)) return CVATTN_ERR_UNSUPPORTED;
+    if (dst->ne[0] != src->ne[0] || dst->ne[0] % type_block(dst->type)) return CVATTN_ERR_BAD_ARGS;
+    if (dst->ne[2] != src->ne[2] || dst->ne[3] != src->ne[3]) return CVATTN_ERR_BAD_ARGS;
+    if (idx->ne[0] != src->ne[1]) return CVATTN_ERR_BAD_ARGS;
+    if (idx->ne[1] <= 0 || idx->ne[2] <= 0 || src->ne[2] % idx->ne[1] || src->ne[3] % idx->ne[2])
+        return CVATTN_ERR_BAD_ARGS;
+    for (int i = 0; i < 4; i++)
+        if (src->ne[i] < 0 || dst->ne[i] <= 0) return CVATTN_ERR_BAD_ARGS;
+    if (src->ne[1] > 0 && (!dst->data || !src->data || !idx->data)) return CVATTN_ERR_BAD_ARGS;
+    return CVATTN_OK;
+}
+
+CVATTN_API int cvattn_supports_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
+                                        const cvattn_tensor *idx) {
+    return check_set_rows(dst, src, idx) == CVATTN_OK ? 1 : 0;
+}
+
+CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
+                               const cvattn_tensor *idx, cvattn_stream_t stream) {
+    int rc = check_set_rows(dst, src, idx);
+    if (rc) return rc;
+    SetRowsArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.dst = (uint8_t *)dst->data;
+    a.src = (const uint8_t *)src->data;
+    a.idx = (const uint8_t *)idx->data;
+    a.ne0 = src->ne[0];
+    a.n_rows = src->ne[1];
+    a.ne2 = src->ne[2];
+    a.ne3 = src->ne[3];
+    a.dst_rows = dst->ne[1];
+    a.dst_nb1 = (int64_t)dst->nb[1];
+    a.dst_nb2 = (int64_t)dst->nb[2];
+    a.dst_nb3 = (int64_t)dst->nb[3];
+    a.src_nb1 = (int64_t)src->nb[1];
+    a.src_nb2 = (int64_t)src->nb[2];
+    a.src_nb3 = (int64_t)src->nb[3];
+    a.idx_nb0 = (int64_t)idx->nb[0];
+    a.idx_nb1 = (int64_t)idx->nb[1];
+    a.idx_nb2 = (int64_t)idx->nb[2];
+    a.idx_ne1 = idx->ne[1];
+    a.idx_ne2 = idx->ne[2];
+    a.idx_i64 = idx->type == 27 ? 1 : 0;
+    const int64_t per = type_block(dst->type) == QK ? QK : 1;
+    a.total = (src->ne[0] / per) * src->ne[1] * src->ne[2] * src->ne[3];
+    return hip_status(set_rows_launch(dst->type, a, (hipStream_t)stream));
+}
+
+CVATTN_API const char *cvattn_status_string(int status) {
+    switch (status) {
+    case CVATTN_OK: return "ok";
+    case CVATTN_ERR_UNSUPPORTED: return "unsupported";
+    case CVATTN_ERR_BAD_ARGS: return "bad arguments";
+    case CVATTN_ERR_WORKSPACE_TOO_SMALL: return "workspace too small";
+    case CVATTN_ERR_HIP: return "hip error";
+    default: return "unknown status";
+    }
+}
+
+} // extern "C"

@@ -1,0 +1,94 @@
+// cvattn_common.h -- types shared by the host dispatcher and the gfx950 kernels.
+//
+// Block formats are ggml's (ggml-common.h), as cosyvoice.cpp stores them in its KV cache
+// (src/cosyvoice-kv-cache.cpp:104-119, types chosen at src/cosyvoice-loader.cpp:468-510):
+//   q8_0 {f16 d; i8 qs[32]}                   34 B   x = qs*d
+//   q4_0 {f16 d; u8 qs[16]}                   18 B   x = (nib-8)*d
+//   q4_1 {f16 d; f16 m; u8 qs[16]}            20 B   x = nib*d + m
+//   q5_0 {f16 d; u8 qh[4]; u8 qs[16]}         22 B   x = (nib|hb<<4 - 16)*d
+//   q5_1 {f16 d; f16 m; u8 qh[4]; u8 qs[16]}  24 B   x = (nib|hb<<4)*d + m
+// Element j<16 of a 4/5-bit block is the low nibble of qs[j], element j+16 the high nibble;
+// its 5th bit is bit j (resp. j+16) of qh.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+namespace cvattn {
+
+enum : int {
+    T_F32 = 0,
+    T_F16 = 1,
+    T_Q4_0 = 2,
+    T_Q4_1 = 3,
+    T_Q5_0 = 6,
+    T_Q5_1 = 7,
+    T_Q8_0 = 8,
+    T_I32 = 26,
+};
+
+constexpr int QK = 32;   // elements per quantized block
+constexpr int HEAD = 64; // D = Dv handled by the attention kernels
+
+__host__ __device__ constexpr int type_block(int t) {
+    return (t == T_F32 || t == T_F16) ? 1
+           : (t == T_Q4_0 || t == T_Q4_1 || t == T_Q5_0 || t == T_Q5_1 || t == T_Q8_0) ? QK
+                                                                                     : 0;
+}
+__host__ __device__ constexpr int type_bytes(int t) {
+    return t == T_F32 ? 4 : t == T_F16 ? 2 : t == T_Q4_0 ? 18 : t == T_Q4_1 ? 20
+         : t == T_Q5_0 ? 22 : t == T_Q5_1 ? 24 : t == T_Q8_0 ? 34 : 0;
+}
+// Codes are staged as fp16 "1024 + u" (u the unsigned code); the true code is u - code_off.
+__host__ __device__ constexpr int code_off(int t) {
+    return t == T_Q8_0 ? 128 : t == T_Q4_0 ? 8 : t == T_Q5_0 ? 16 : 0;
+}
+__host__ __device__ constexpr bool has_min(int t) { return t == T_Q4_1 || t == T_Q5_1; }
+__host__ __device__ constexpr bool is_quant(int t) { return type_block(t) == QK; }
+
+// One attention problem as the kernels see it (strides in bytes; nb0 is implied by the type).
+struct FaProblem {
+    const void *q;
+    const void *k;
+    const void *v;
+    const void *mask; // f16 or nullptr
+    float *dst;       // f32 contiguous [Dv, H, n_q, B]
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int32_t m_ne2, m_ne3;
+    int32_t n_kv;
+    int32_t n_splits;
+    int32_t split_len;    // tokens per split (multiple of the kernel's token step)
+    int32_t rk3, rv3;     // B / B_k, B / B_v
+    int64_t unit_begin;   // first workgroup unit of this problem in the launch
+    int64_t part_begin;   // first partial slot (rows) of this problem in the workspace
+    int64_t row_begin;    // first output row (b, i, h) of this problem (combine indexing)
+    int64_t cnt_begin;    // first split-arrival counter of this problem (prepared batches)
+};
+
+// Parameters shared by every problem of one launch.
+struct FaUniform {
+    int32_t n_q, H, H_kv, G, B;
+    int32_t n_rows;      // n_q * G rows per (batch, kv head)
+    int32_t n_rowgroups; // ceil(n_rows / rows per workgroup)
+    int32_t q_f16;       // Q element type: 0 f32, 1 f16
+    int32_t n_problems;
+    float scale_log2;    // scale * log2(e)
+    int64_t total_units;
+    int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)
+    float *partials;     // workspace: split partial (m, l, O[64]) per row slot
+    uint32_t *counters;  // prepared batches: split-arrival counter per (problem, b, kh, row group),
+                         // zero between launches (the merging workgroup resets its counter)
+};
+
+constexpr int PART_STRIDE = 68; // floats per partial slot: O[64], m, l, pad
+
+struct FaArgs {
+    FaUniform u;
+    FaProblem p0;              // used when n_problems == 1
+    const FaProblem *table;    // device table when n_problems > 1
+};
+
+} // namespace cvattn

@@ -1,0 +1,39 @@
+// cvattn_launch.h -- internal launchers implemented in the .hip translation units.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include "cvattn_common.h"
+
+namespace cvattn {
+
+// Workgroup shape chosen for a problem: decode-shaped (<= 16 rows per kv head, waves split the
+// tokens) or row-tiled (waves split the rows).
+struct FaKernelShape {
+    bool wsplit;
+    int nw;             // waves per workgroup
+    int tstep;          // tokens per staged tile (per wave when wsplit)
+    int rows_per_group; // query rows per workgroup
+};
+FaKernelShape fa_shape(int n_rows);
+hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
+                     hipStream_t st);
+
+hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st);
+
+struct SetRowsArgs {
+    uint8_t *dst;
+    const uint8_t *src;
+    const uint8_t *idx;
+    int64_t ne0, n_rows, ne2, ne3;
+    int64_t dst_rows;
+    int64_t dst_nb1, dst_nb2, dst_nb3;
+    int64_t src_nb1, src_nb2, src_nb3;
+    int64_t idx_nb0, idx_nb1, idx_nb2;
+    int64_t idx_ne1, idx_ne2;
+    int32_t idx_i64;
+    int64_t total;
+};
+hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st);
+
+} // namespace cvattn

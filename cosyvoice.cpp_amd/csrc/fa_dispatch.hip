@@ -1,0 +1,39 @@
+// fa_dispatch.hip -- picks the flash-attention instantiation for a launch.
+#include "fa_impl.h"
+
+namespace cvattn {
+
+FaLaunchFn fa_pick_decode(int mask, int batch, int ki, int vi);
+FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
+
+static int type_index(int t) {
+    switch (t) {
+    case T_F32: return 0;
+    case T_F16: return 1;
+    case T_Q8_0: return 2;
+    case T_Q4_0: return 3;
+    case T_Q4_1: return 4;
+    case T_Q5_0: return 5;
+    case T_Q5_1: return 6;
+    default: return -1;
+    }
+}
+
+FaKernelShape fa_shape(int n_rows) {
+    FaKernelShape s;
+    s.wsplit = n_rows <= 16;
+    s.nw = 4;
+    s.tstep = s.wsplit ? FaCfg<4, true>::TSTEP : FaCfg<4, false>::TSTEP;
+    s.rows_per_group = s.wsplit ? FaCfg<4, true>::ROWS : FaCfg<4, false>::ROWS;
+    return s;
+}
+
+hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
+                     hipStream_t st) {
+    const int ki = type_index(ktype), vi = type_index(vtype);
+    if (ki < 0 || vi < 0) return hipErrorInvalidValue;
+    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
+    return fn(a, st);
+}
+
+} // namespace cvattn

@@ -1,0 +1,215 @@
+// kv_kernels.hip -- KV-cache block formats on gfx950:
+//   * dequantize: the test entry for the in-register unpacking the attention kernels use
+//     (same raw8_load/raw8_unpack path), bit-exact to ggml's dequantize_row_*;
+//   * set_rows: the quantize-on-write KV update of cosyvoice_kv_cache::update_cache
+//     (src/cosyvoice-kv-cache.cpp:316,322), bit-exact to ggml's quantize_row_*_ref.
+#include "cvattn_device.h"
+#include "cvattn_launch.h"
+
+namespace cvattn {
+
+// One thread per 8 elements of a 32-element block (f16 shares the 32-element grouping).
+template <int T>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *src, float *dst, int64_t n_groups) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t blk = gid >> 2;
+    if (blk >= n_groups) return;
+    const int c = (int)(gid & 3);
+    const int64_t row_bytes = T == T_F16 ? 64 : type_bytes(T);
+    Raw8 r;
+    raw8_load<T>(src + blk * row_bytes, 0, c, r);
+    uint32_t o[4];
+    raw8_unpack<T>(r, c, o);
+    constexpr float bias = stage_bias<T>();
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const h2 h = __builtin_bit_cast(h2, o[i]);
+#pragma unroll
+        for (int s = 0; s < 2; s++) {
+            if constexpr (is_quant(T)) {
+                // (code)*d is exact in fp32; only "+ m" rounds, as in ggml's dequantizers
+                const float code = (float)h[s] - bias;
+                y[2 * i + s] = has_min(T) ? code * r.d + r.m : code * r.d;
+            } else {
+                y[2 * i + s] = (float)h[s];
+            }
+        }
+    }
+    float *out = dst + blk * 32 + 8 * c;
+#pragma unroll
+    for (int i = 0; i < 8; i++) out[i] = y[i];
+}
+
+__global__ __launch_bounds__(256) void copy_f32_kernel(const float *src, float *dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16 *src, float *dst, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = (float)src[i];
+}
+
+// ------------------------------------------------------------------------------------------
+// ggml quantize_row_*_ref, one 32-element block per thread.  Contraction is disabled so each
+// multiply/add rounds exactly like the reference C (x*id then +8.5f are separate roundings).
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void st_half(uint8_t *p, float f) {
+    const _Float16 h = (_Float16)f;
+    __builtin_memcpy(p, &h, 2);
+}
+
+template <int T>
+__device__ void quantize_block_ref(const float *x, uint8_t *y) {
+#pragma clang fp contract(off)
+    if constexpr (T == T_Q8_0) {
+        float amax = 0.0f;
+        for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_half(y, d);
+        for (int j = 0; j < 32; j++) y[2 + j] = (uint8_t)(int8_t)roundf(x[j] * id);
+    } else if constexpr (T == T_Q4_0 || T == T_Q5_0) {
+        constexpr float nlev = T == T_Q4_0 ? -8.0f : -16.0f;
+        constexpr float off = T == T_Q4_0 ? 8.5f : 16.5f;
+        constexpr int qmax = T == T_Q4_0 ? 15 : 31;
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 32; j++) {
+            const float v = x[j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / nlev;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_half(y, d);
+        uint32_t qh = 0;
+        const int qs_off = T == T_Q4_0 ? 2 : 6;
+        for (int j = 0; j < 16; j++) {
+            const float x0 = x[j] * id;
+            const float x1 = x[j + 16] * id;
+            const int q0 = min(qmax, (int)(int8_t)(int)(x0 + off));
+            const int q1 = min(qmax, (int)(int8_t)(int)(x1 + off));
+            const uint8_t u0 = (uint8_t)q0, u1 = (uint8_t)q1;
+            y[qs_off + j] = (uint8_t)((u0 & 0x0f) | ((u1 & 0x0f) << 4));
+            qh |= ((uint32_t)(u0 & 0x10u) >> 4) << j;
+            qh |= ((uint32_t)(u1 & 0x10u) >> 4) << (j + 16);
+        }
+        if constexpr (T == T_Q5_0) __builtin_memcpy(y + 2, &qh, 4);
+    } else if constexpr (T == T_Q4_1 || T == T_Q5_1) {
+        constexpr float nlev = T == T_Q4_1 ? 15.0f : 31.0f;
+        float mn = 3.402823466e+38f, mx = -3.402823466e+38f;
+        for (int j = 0; j < 32; j++) {
+            const float v = x[j];
+            if (v < mn) mn = v;
+            if (v > mx) mx = v;
+        }
+        const float d = (mx - mn) / nlev;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        st_half(y, d);
+        st_half(y + 2, mn);
+        uint32_t qh = 0;
+        const int qs_off = T == T_Q4_1 ? 4 : 8;
+        for (int j = 0; j < 16; j++) {
+            const float x0 = (x[j] - mn) * id;
+            const float x1 = (x[j + 16] - mn) * id;
+            uint8_t u0, u1;
+            if constexpr (T == T_Q4_1) {
+                u0 = (uint8_t)min(15, (int)(int8_t)(int)(x0 + 0.5f));
+                u1 = (uint8_t)min(15, (int)(int8_t)(int)(x1 + 0.5f));
+            } else {
+                u0 = (uint8_t)(int)(x0 + 0.5f);
+                u1 = (uint8_t)(int)(x1 + 0.5f);
+            }
+            y[qs_off + j] = (uint8_t)((u0 & 0x0f) | ((u1 & 0x0f) << 4));
+            qh |= ((uint32_t)(u0 & 0x10u) >> 4) << j;
+            qh |= ((uint32_t)(u1 & 0x10u) >> 4) << (j + 16);
+        }
+        if constexpr (T == T_Q5_1) __builtin_memcpy(y + 4, &qh, 4);
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(256) void set_rows_kernel(SetRowsArgs a) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= a.total) return;
+    constexpr int per = is_quant(T) ? 32 : 1;
+    const int64_t units_per_row = a.ne0 / per;
+    const int64_t e = gid % units_per_row;
+    int64_t r = gid / units_per_row;
+    const int64_t i01 = r % a.n_rows;
+    r /= a.n_rows;
+    const int64_t i02 = r % a.ne2;
+    const int64_t i03 = r / a.ne2;
+    const uint8_t *ip = a.idx + i01 * a.idx_nb0 + (i02 % a.idx_ne1) * a.idx_nb1 + (i03 % a.idx_ne2) * a.idx_nb2;
+    int64_t i1;
+    if (a.idx_i64) {
+        __builtin_memcpy(&i1, ip, 8);
+    } else {
+        int32_t v;
+        __builtin_memcpy(&v, ip, 4);
+        i1 = v;
+    }
+    if (i1 < 0 || i1 >= a.dst_rows) return; // out-of-range positions write nothing
+    const float *x = (const float *)(a.src + i01 * a.src_nb1 + i02 * a.src_nb2 + i03 * a.src_nb3) + e * per;
+    uint8_t *y = a.dst + i1 * a.dst_nb1 + i02 * a.dst_nb2 + i03 * a.dst_nb3 + e * type_bytes(T);
+    if constexpr (T == T_F32) {
+        __builtin_memcpy(y, x, 4);
+    } else if constexpr (T == T_F16) {
+        st_half(y, *x);
+    } else {
+        float xb[32];
+        for (int j = 0; j < 32; j++) xb[j] = x[j];
+        quantize_block_ref<T>(xb, y);
+    }
+}
+
+// ------------------------------------------------------------------------------------------
+// Host launchers.
+// ------------------------------------------------------------------------------------------
+hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    if (type == T_F32) {
+        hipLaunchKernelGGL(copy_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           (const float *)src, dst, n);
+        return hipGetLastError();
+    }
+    if (type == T_F16 && (n % 32) != 0) {
+        hipLaunchKernelGGL(f16_to_f32_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                           (const _Float16 *)src, dst, n);
+        return hipGetLastError();
+    }
+    const int64_t groups = n / 32;
+    const unsigned grid = (unsigned)((groups * 4 + 255) / 256);
+    const uint8_t *s = (const uint8_t *)src;
+    switch (type) {
+    case T_F16: hipLaunchKernelGGL(dequant_kernel<T_F16>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    case T_Q8_0: hipLaunchKernelGGL(dequant_kernel<T_Q8_0>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    case T_Q4_0: hipLaunchKernelGGL(dequant_kernel<T_Q4_0>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    case T_Q4_1: hipLaunchKernelGGL(dequant_kernel<T_Q4_1>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    case T_Q5_0: hipLaunchKernelGGL(dequant_kernel<T_Q5_0>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    case T_Q5_1: hipLaunchKernelGGL(dequant_kernel<T_Q5_1>, dim3(grid), dim3(256), 0, st, s, dst, groups); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st) {
+    if (a.total <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((a.total + 255) / 256)), block(256);
+    switch (type) {
+    case T_F32: hipLaunchKernelGGL(set_rows_kernel<T_F32>, grid, block, 0, st, a); break;
+    case T_F16: hipLaunchKernelGGL(set_rows_kernel<T_F16>, grid, block, 0, st, a); break;
+    case T_Q8_0: hipLaunchKernelGGL(set_rows_kernel<T_Q8_0>, grid, block, 0, st, a); break;
+    case T_Q4_0: hipLaunchKernelGGL(set_rows_kernel<T_Q4_0>, grid, block, 0, st, a); break;
+    case T_Q4_1: hipLaunchKernelGGL(set_rows_kernel<T_Q4_1>, grid, block, 0, st, a); break;
+    case T_Q5_0: hipLaunchKernelGGL(set_rows_kernel<T_Q5_0>, grid, block, 0, st, a); break;
+    case T_Q5_1: hipLaunchKernelGGL(set_rows_kernel<T_Q5_1>, grid, block, 0, st, a); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+} // namespace cvattn

@@ -1,0 +1,168 @@
+/*
+ * cvattn.h -- C ABI of the MI355X (gfx950) attention engine for cosyvoice.cpp.
+ *
+ * The engine replaces the GGML_OP_FLASH_ATTN_EXT nodes that cosyvoice.cpp builds at
+ *   src/cosyvoice-kv-cache.cpp:383-384   (LLM decode/prefill over the KV cache, and the DiT
+ *                                         streaming-cache path)
+ *   src/cosyvoice-graph.cpp:375-376      (DiT attention without a cache)
+ * and the GGML_OP_SET_ROWS KV write at src/cosyvoice-kv-cache.cpp:316,322, plus the backend
+ * capability probes at src/cosyvoice-loader.cpp:555-566.
+ *
+ * Tensors are described exactly as ggml describes them (data, type, ne[4], nb[4] in bytes), so
+ * a ggml backend can forward a node's src[] tensors field by field.  Type codes are ggml_type
+ * values.  All entry points are reentrant, keep no state between calls, never allocate device
+ * memory and never abort: failures come back as cvattn_status codes.  Only the set-up call
+ * cvattn_fa_batch_prepare waits for the device.  Pointers in descriptors are device pointers.
+ */
+#ifndef CVATTN_H
+#define CVATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#if defined(_WIN32)
+#define CVATTN_API __declspec(dllexport)
+#else
+#define CVATTN_API __attribute__((visibility("default")))
+#endif
+
+/* hipStream_t is `struct ihipStream_t *`; declared here so callers need no HIP headers. */
+struct ihipStream_t;
+typedef struct ihipStream_t *cvattn_stream_t;
+
+/* ggml_type values of the KV cache formats (include/cosyvoice.h:32-42 lists the same set). */
+typedef enum cvattn_type {
+    CVATTN_TYPE_F32 = 0,
+    CVATTN_TYPE_F16 = 1,
+    CVATTN_TYPE_Q4_0 = 2,
+    CVATTN_TYPE_Q4_1 = 3,
+    CVATTN_TYPE_Q5_0 = 6,
+    CVATTN_TYPE_Q5_1 = 7,
+    CVATTN_TYPE_Q8_0 = 8,
+    CVATTN_TYPE_I32 = 26,
+} cvattn_type;
+
+/* ggml_prec values accepted by cvattn_flash_attn_ext (all math is fp32-accumulated). */
+#define CVATTN_PREC_DEFAULT 0
+#define CVATTN_PREC_F32 10
+
+typedef enum cvattn_status {
+    CVATTN_OK = 0,
+    CVATTN_ERR_UNSUPPORTED = 1,
+    CVATTN_ERR_BAD_ARGS = 2,
+    CVATTN_ERR_WORKSPACE_TOO_SMALL = 3,
+    CVATTN_ERR_HIP = 4,
+} cvattn_status;
+
+/* Mirrors ggml_tensor's data/type/ne/nb. */
+typedef struct cvattn_tensor {
+    void *data;
+    int32_t type;
+    int64_t ne[4];
+    size_t nb[4];
+} cvattn_tensor;
+
+/* --------------------------------------------------------------------------------------------
+ * Flash attention: dst = softmax(scale * Q K^T + mask) V, the ggml_flash_attn_ext contract.
+ *   q    f32|f16 [D, n_q, H, B]            (any strides)
+ *   k    f32|f16|q8_0|q4_0|q4_1|q5_0|q5_1 [D, n_kv, H_kv, B_k]   (nb0 = element or block size;
+ *        a head row of a block type is D/32 consecutive blocks)
+ *   v    same type set, [Dv, n_kv, H_kv, B_v]
+ *   mask NULL or f16 [>= n_kv, >= n_q, 1|H, 1|B]; row index = local query index; -inf drops a key
+ *   dst  f32 contiguous [Dv, H, n_q, B]
+ * H % H_kv == 0 and the kv head of q head h is h / (H / H_kv); B % B_k == 0.
+ * A query row whose keys are all masked yields 0.  D = Dv = 64 (the head size of every attention
+ * site in cosyvoice.cpp); other sizes are reported unsupported.  max_bias and logit_softcap must
+ * be 0 (cosyvoice.cpp always passes 0, src/cosyvoice-kv-cache.cpp:383, src/cosyvoice-graph.cpp:375).
+ * n_kv is read from k->ne[1] at call time (the reference grows it in place between decode steps,
+ * src/cosyvoice-kv-cache.cpp:398-408).
+ * -------------------------------------------------------------------------------------------- */
+
+/* Replaces ggml_backend_supports_op(backend, ggml_flash_attn_ext(...)) as used by
+ * cosyvoice_check_kv_cache_types, src/cosyvoice-loader.cpp:543-567. */
+CVATTN_API int cvattn_supports_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
+                                              const cvattn_tensor *v, const cvattn_tensor *mask);
+
+/* Bytes of device workspace cvattn_flash_attn_ext needs for these shapes (the partial results
+ * of a KV sequence split over several workgroups).  0 is a valid answer. */
+CVATTN_API size_t cvattn_flash_attn_ext_workspace(const cvattn_tensor *q, const cvattn_tensor *k,
+                                                  const cvattn_tensor *v, const cvattn_tensor *mask);
+
+/* Replaces the GGML_OP_FLASH_ATTN_EXT node built by ggml_flash_attn_ext(ctx, q, k, v, mask,
+ * scale, max_bias, logit_softcap) + ggml_flash_attn_ext_set_prec(node, prec) at
+ * src/cosyvoice-kv-cache.cpp:383-384 and src/cosyvoice-graph.cpp:375-376.  Asynchronous on
+ * `stream`; `ws` must hold cvattn_flash_attn_ext_workspace() bytes (may be NULL when that is 0). */
+CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
+                                     const cvattn_tensor *v, const cvattn_tensor *mask,
+                                     const cvattn_tensor *dst, float scale, float max_bias,
+                                     float logit_softcap, int prec, void *ws, size_t ws_bytes,
+                                     cvattn_stream_t stream);
+
+/* --------------------------------------------------------------------------------------------
+ * Batched flash attention: many independent ggml_flash_attn_ext problems in one launch.
+ * cosyvoice.cpp runs one FA node per layer per worker (src/cosyvoice-llm.cpp:247-255,
+ * src/cosyvoice-model.cpp:102-107); serving several workers or sequences at once
+ * (tools/server/cosyvoice-server.cpp:318-323) gives many such nodes per step.  All problems must
+ * share q/k/v/mask presence and types, D/Dv, H, H_kv, n_q and B; n_kv, pointers and strides may
+ * differ per problem (ragged KV lengths).
+ *   cvattn_fa_batch_workspace   bytes needed for n problems (includes the device problem table)
+ *   cvattn_fa_batch_prepare     validates the problems, uploads the problem table and zeroed
+ *                               split counters into ws (one host->device copy on `stream`, then
+ *                               waits for it: a set-up call) and fills a host-side plan
+ *   cvattn_fa_batch_launch      runs a prepared plan: one kernel launch, split partials merged by
+ *                               the last workgroup of each split group (no host->device traffic;
+ *                               may be called repeatedly, or captured in a HIP graph, while ws and
+ *                               the tensors stay valid; launches sharing one ws must not overlap)
+ * -------------------------------------------------------------------------------------------- */
+typedef struct cvattn_fa_problem {
+    cvattn_tensor q, k, v, mask, dst; /* mask.data == NULL: no mask */
+} cvattn_fa_problem;
+
+/* Opaque launch plan filled by cvattn_fa_batch_prepare (caller-owned host memory). */
+typedef struct cvattn_fa_plan {
+    uint64_t opaque[64];
+} cvattn_fa_plan;
+
+CVATTN_API size_t cvattn_fa_batch_workspace(const cvattn_fa_problem *problems, int n);
+CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n, float scale,
+                                       void *ws, size_t ws_bytes, cvattn_stream_t stream,
+                                       cvattn_fa_plan *plan);
+CVATTN_API int cvattn_fa_batch_launch(const cvattn_fa_plan *plan, cvattn_stream_t stream);
+
+/* --------------------------------------------------------------------------------------------
+ * Block formats.
+ * -------------------------------------------------------------------------------------------- */
+
+/* Elements per block (32 for q*, 1 for f16/f32) and bytes per block; 0 for unknown types. */
+CVATTN_API int64_t cvattn_block_size(int type);
+CVATTN_API int64_t cvattn_type_size(int type);
+
+/* dst[0..n) = dequantized src (ggml's dequantize_row_* for `type`); n % block size == 0.
+ * Test entry for the in-register dequantizers the attention kernels use. */
+CVATTN_API int cvattn_dequantize(int type, const void *src, float *dst, int64_t n,
+                                 cvattn_stream_t stream);
+
+/* --------------------------------------------------------------------------------------------
+ * KV write: the GGML_OP_SET_ROWS node of cosyvoice_kv_cache::update_cache
+ * (src/cosyvoice-kv-cache.cpp:316,322): dst[:, idx[i], i2, i3] = quantize_ref(src[:, i, i2, i3]).
+ *   dst  cache tensor of a KV type, [ne0, rows, ne2, ne3]
+ *   src  f32 [ne0, n, ne2, ne3]
+ *   idx  i32 [n] (positions; ggml broadcasts a 1-D index over ne2/ne3)
+ * Quantization follows ggml's quantize_row_*_ref bit for bit.
+ * -------------------------------------------------------------------------------------------- */
+CVATTN_API int cvattn_supports_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
+                                        const cvattn_tensor *idx);
+CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
+                               const cvattn_tensor *idx, cvattn_stream_t stream);
+
+/* Human-readable name of a status code. */
+CVATTN_API const char *cvattn_status_string(int status);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,129 @@
+"""CPU-side checks of the C ABI: the library loads, exports every entry point include/cvattn.h
+declares, and its host-side validation (the supports_op probe, workspace sizing, error codes)
+behaves like ggml's shape rules.  No kernel is launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import cvattn
+from cvattn import F16, F32, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "cvattn.h")
+FAKE = 0x1000  # never dereferenced: validation-only calls
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"CVATTN_API\s+[\w\s\*]+?\b(cvattn_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported(eng):
+    syms = header_symbols()
+    assert len(syms) >= 12
+    for s in syms:
+        assert hasattr(eng.L, s), s
+    assert set(syms) == set(cvattn.EXPORTED)
+
+
+def test_type_table(eng):
+    for t, (blk, size) in {F32: (1, 4), F16: (1, 2), Q8_0: (32, 34), Q4_0: (32, 18), Q4_1: (32, 20),
+                           Q5_0: (32, 22), Q5_1: (32, 24)}.items():
+        assert eng.block_size(t) == blk and eng.type_size(t) == size
+    assert eng.block_size(99) == 0 and eng.type_size(99) == 0
+
+
+def llm(n_q=1, n_kv=512, kt=Q8_0, vt=Q4_0, H=14, Hkv=2, max_seq=4096):
+    q = cvattn.llm_q_view(FAKE, 64, H, n_q)
+    k = cvattn.llm_kv_view(FAKE, kt, 64, Hkv, n_kv, max_seq)
+    v = cvattn.llm_kv_view(FAKE, vt, 64, Hkv, n_kv, max_seq)
+    dst = cvattn.out_view(FAKE, 64, H, n_q)
+    return q, k, v, dst
+
+
+@pytest.mark.parametrize("kt", [F32, F16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1])
+@pytest.mark.parametrize("vt", [F32, F16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1])
+def test_supports_every_kv_type_pair(eng, kt, vt):
+    """Every type the loader's fallback chain can pick (src/cosyvoice-loader.cpp:498-510)."""
+    q, k, v, _ = llm(kt=kt, vt=vt)
+    assert eng.supports_flash_attn_ext(q, k, v, None)
+
+
+def test_supports_rejects(eng):
+    q, k, v, _ = llm()
+    bad = cvattn.llm_kv_view(FAKE, Q8_0, 128, 1, 512, 4096)  # head size 128
+    assert not eng.supports_flash_attn_ext(q, bad, v, None)
+    k26 = cvattn.tensor(FAKE, 26, list(k.ne), list(k.nb))  # i32 keys
+    assert not eng.supports_flash_attn_ext(q, k26, v, None)
+    q3 = cvattn.llm_q_view(FAKE, 64, 15, 1)  # 15 heads over 2 kv heads
+    assert not eng.supports_flash_attn_ext(q3, k, v, None)
+    m = cvattn.mask_view(FAKE, 100, 1)  # mask shorter than n_kv
+    assert not eng.supports_flash_attn_ext(q, k, v, m)
+    m = cvattn.mask_view(FAKE, 512, 1)
+    assert eng.supports_flash_attn_ext(q, k, v, m)
+    mf32 = cvattn.tensor(FAKE, F32, [512, 1, 1, 1], [4, 2048, 2048, 2048])
+    assert not eng.supports_flash_attn_ext(q, k, v, mf32)
+
+
+def test_probe_shapes_of_loader(eng):
+    """cosyvoice_check_kv_cache_types probes q [64,1,14,1] against a 1-row cache (loader.cpp:543-567)."""
+    for kt in (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, F16, F32):
+        q = cvattn.contiguous(FAKE, F32, [64, 1, 14, 1])
+        k = cvattn.llm_kv_view(FAKE, kt, 64, 2, 1, 1)
+        v = cvattn.llm_kv_view(FAKE, kt, 64, 2, 1, 1)
+        assert eng.supports_flash_attn_ext(q, k, v, None)
+
+
+def test_workspace_and_errors(eng):
+    q, k, v, dst = llm(n_kv=4096)
+    ws = eng.flash_attn_ext_workspace(q, k, v, None)
+    assert ws > 0  # long decode is split over the chip
+    assert eng.flash_attn_ext(q, k, v, None, dst, 0.125, 0, 0) == cvattn.ERR_WORKSPACE_TOO_SMALL
+    assert eng.flash_attn_ext(q, k, v, None, dst, 0.125, FAKE, ws, max_bias=1.0) == cvattn.ERR_UNSUPPORTED
+    assert eng.flash_attn_ext(q, k, v, None, dst, 0.125, FAKE, ws, softcap=30.0) == cvattn.ERR_UNSUPPORTED
+    assert eng.flash_attn_ext(q, k, v, None, dst, float("nan"), FAKE, ws) == cvattn.ERR_BAD_ARGS
+    bad_dst = cvattn.out_view(FAKE, 64, 14, 2)
+    assert eng.flash_attn_ext(q, k, v, None, bad_dst, 0.125, FAKE, ws) == cvattn.ERR_BAD_ARGS
+    assert eng.status_string(cvattn.ERR_WORKSPACE_TOO_SMALL) == "workspace too small"
+    # tiny problems need no workspace
+    q, k, v, dst = llm(n_kv=64)
+    assert eng.flash_attn_ext_workspace(q, k, v, None) == 0
+
+
+def test_batch_validation(eng):
+    probs = []
+    for n_kv in (256, 1000, 8192):
+        q, k, v, dst = llm(n_kv=n_kv, kt=Q8_0, vt=Q8_0, max_seq=8192)
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.dst = q, k, v, dst
+        probs.append(p)
+    ws = eng.fa_batch_workspace(probs)
+    assert ws > 0
+    rc, _ = eng.fa_batch_prepare(probs, 0.125, 0, 0)
+    assert rc == cvattn.ERR_WORKSPACE_TOO_SMALL
+    q, k, v, dst = llm(n_kv=10, kt=Q8_0, vt=Q4_0)  # a different V type cannot join the batch
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.dst = q, k, v, dst
+    assert eng.fa_batch_workspace(probs + [p]) == 0
+
+
+def test_set_rows_validation(eng):
+    dst = cvattn.contiguous(FAKE, Q8_0, [128, 4096, 1, 1])
+    src = cvattn.contiguous(FAKE, F32, [128, 3, 1, 1])
+    idx = cvattn.contiguous(FAKE, 26, [3, 1, 1, 1])
+    assert eng.supports_set_rows(dst, src, idx)
+    src_bad = cvattn.contiguous(FAKE, F32, [96, 3, 1, 1])
+    assert not eng.supports_set_rows(dst, src_bad, idx)
+    dst40 = cvattn.contiguous(FAKE, F16, [40, 16, 1, 1])
+    src40 = cvattn.contiguous(FAKE, F32, [40, 3, 1, 1])
+    assert eng.supports_set_rows(dst40, src40, idx)  # f16 rows need no block alignment
+    dstq40 = cvattn.contiguous(FAKE, F16, [40, 16, 1, 1])
+    dstq40.type = Q4_0
+    assert not eng.supports_set_rows(dstq40, src40, idx)
+
+
+def test_library_is_loaded_from_tree(eng):
+    assert os.path.dirname(eng.path) == os.path.join(ROOT, "cosyvoice.cpp_amd")
+    assert isinstance(eng.L, ctypes.CDLL)

@@ -1,0 +1,302 @@
+"""GPU parity of cvattn_flash_attn_ext (the GGML_OP_FLASH_ATTN_EXT node) against the fp64 oracle,
+with the exact tensor views the reference builds:
+  LLM decode/prefill  src/cosyvoice-kv-cache.cpp:316-324, src/cosyvoice-llm.cpp:56-60
+  DiT (no cache)      src/cosyvoice-graph.cpp:357-377
+  DiT (stream cache)  src/cosyvoice-graph.cpp:363-367 -> kv-cache views with batch 2
+Bar: max-abs <= 2e-3 and mean-abs <= 2e-4 vs the fp64 oracle on identical (bit-exact) inputs."""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import cvattn
+from _gpu import check_close, dev, empty_f32, host, run_fa, workspace
+from oracle.oracle import F16, F32, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, TYPE_BYTES, row_bytes, view
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+D = 64
+ALL_TYPES = [F32, F16, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1]
+
+
+class Case:
+    """One attention problem held twice: host buffers for the oracle, device buffers for the engine,
+    both described with the same ne/nb."""
+
+    def __init__(self):
+        self.keep = []
+
+    def add(self, name, arr, ttype, ne, nb):
+        arr = np.ascontiguousarray(arr)
+        d = dev(arr)
+        self.keep += [arr, d]
+        setattr(self, name + "_h", view(arr, ttype, ne, nb))
+        setattr(self, name + "_d", cvattn.tensor(d.data_ptr(), ttype, ne, nb))
+        setattr(self, name + "_dev", d)
+
+
+def kv_bytes(orc, t, x):
+    """[..., rows, H_kv*D] float32 -> [..., rows, row_bytes] cache bytes."""
+    lead = x.shape[:-1]
+    flat = orc.quantize_flat(t, x.reshape(-1))
+    return flat.reshape(*lead, row_bytes(t, x.shape[-1]))
+
+
+def llm_case(orc, rng, *, H=14, Hkv=2, nq=1, nkv=512, kt=F16, vt=F16, B=1, kB=None, max_seq=None,
+             mask=None, qscale=1.0, kvscale=1.0):
+    kB = kB or B
+    max_seq = max_seq or nkv
+    c = Case()
+    q = (qscale * rng.standard_normal((B, nq, H, D))).astype(np.float32)
+    c.add("q", q, F32, [D, nq, H, B], [4, 4 * D * H, 4 * D, 4 * D * H * nq])
+    for name, t in (("k", kt), ("v", vt)):
+        x = (kvscale * rng.standard_normal((kB, max_seq, Hkv * D))).astype(np.float32)
+        b = kv_bytes(orc, t, x)
+        rb = row_bytes(t, Hkv * D)
+        c.add(name, b, t, [D, nkv, Hkv, kB], [TYPE_BYTES[t], rb, rb // Hkv, rb * max_seq])
+    c.mask_h = c.mask_d = None
+    if mask is not None:
+        m = np.ascontiguousarray(mask)
+        ne = [m.shape[-1], m.shape[-2], m.shape[-3] if m.ndim > 2 else 1, m.shape[-4] if m.ndim > 3 else 1]
+        nb = [2, 2 * ne[0], 2 * ne[0] * ne[1], 2 * ne[0] * ne[1] * ne[2]]
+        c.add("mask", m, F16, ne, nb)
+    c.out_shape = (B, nq, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, nq, B)
+    return c
+
+
+def run_case(eng, orc, c, scale=0.125, what=""):
+    run_fa(eng, c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d, scale)
+    got = host(c.dst)
+    want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, scale, c.out_shape)
+    return check_close(got, want, what=what), got, want
+
+
+# ------------------------------------------------------------------------------------------
+# committed fixtures
+# ------------------------------------------------------------------------------------------
+def test_golden_cfg1_decode_f16(eng, cuda):
+    """Config 1: single-layer decode, 14/2 heads, f16 KV, n_kv 512, scale 1/8, no mask."""
+    g = np.load(os.path.join(GOLDEN, "attn_cfg1.npz"))
+    q, kh, vh = g["q"], g["k_f16"], g["v_f16"]
+    dq, dk, dv = dev(q), dev(kh), dev(vh)
+    qd = cvattn.llm_q_view(dq.data_ptr(), D, 14, 1)
+    kd = cvattn.llm_kv_view(dk.data_ptr(), F16, D, 2, 512, 512)
+    vd = cvattn.llm_kv_view(dv.data_ptr(), F16, D, 2, 512, 512)
+    out = empty_f32(14, D)
+    run_fa(eng, qd, kd, vd, None, cvattn.out_view(out.data_ptr(), D, 14, 1))
+    check_close(host(out), g["out"], what="cfg1")
+
+
+def test_golden_prefill_small(eng, cuda):
+    g = np.load(os.path.join(GOLDEN, "attn_prefill_small.npz"))
+    nq, nkv = 8, 40
+    dq, dk, dv, dm = dev(g["q"]), dev(g["k_q8_0"]), dev(g["v_q4_0"]), dev(g["mask"])
+    qd = cvattn.llm_q_view(dq.data_ptr(), D, 14, nq)
+    kd = cvattn.llm_kv_view(dk.data_ptr(), Q8_0, D, 2, nkv, nkv)
+    vd = cvattn.llm_kv_view(dv.data_ptr(), Q4_0, D, 2, nkv, nkv)
+    md = cvattn.mask_view(dm.data_ptr(), nkv, nq)
+    out = empty_f32(nq, 14, D)
+    run_fa(eng, qd, kd, vd, md, cvattn.out_view(out.data_ptr(), D, 14, nq))
+    check_close(host(out), g["out"].reshape(nq, 14, D), what="prefill_small")
+
+
+def test_golden_dit_small(eng, cuda):
+    g = np.load(os.path.join(GOLDEN, "attn_dit_small.npz"))
+    T, B = 40, 2
+    q, k, v = (g[n].astype(np.float32) for n in ("q", "k", "v"))
+    dq, dk, dv, dm = dev(q), dev(k), dev(v), dev(g["mask"])
+    qd = cvattn.dit_view(dq.data_ptr(), T, B)
+    kd = cvattn.dit_view(dk.data_ptr(), T, B)
+    vd = cvattn.dit_view(dv.data_ptr(), T, B)
+    md = cvattn.mask_view(dm.data_ptr(), T, T)
+    out = empty_f32(B, T, 16, D)
+    run_fa(eng, qd, kd, vd, md, cvattn.out_view(out.data_ptr(), D, 16, T, B))
+    check_close(host(out), g["out"], what="dit_small")
+
+
+# ------------------------------------------------------------------------------------------
+# every K/V type pair the loader can choose
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("kt", ALL_TYPES)
+@pytest.mark.parametrize("vt", ALL_TYPES)
+def test_decode_type_pairs(eng, orc, rng, kt, vt, cuda):
+    c = llm_case(orc, rng, nq=1, nkv=301, kt=kt, vt=vt, max_seq=320)
+    run_case(eng, orc, c, what=f"k{kt} v{vt}")
+
+
+@pytest.mark.parametrize("kt,vt", [(Q8_0, Q4_0), (Q8_0, Q8_0), (F16, F16), (Q5_1, Q5_1)])
+def test_decode_config2_layer(eng, orc, rng, kt, vt, cuda):
+    """Config 2 layer shape: n_kv 4096 in a 4096-row cache, 14/2 heads (split over the chip)."""
+    c = llm_case(orc, rng, nq=1, nkv=4096, kt=kt, vt=vt, max_seq=4096)
+    run_case(eng, orc, c, what="cfg2 layer")
+
+
+@pytest.mark.parametrize("nkv", [1, 2, 31, 32, 33, 127, 129, 1000])
+def test_decode_ragged_lengths(eng, orc, rng, nkv, cuda):
+    c = llm_case(orc, rng, nq=1, nkv=nkv, kt=Q8_0, vt=Q4_0, max_seq=nkv + 40)
+    run_case(eng, orc, c, what=f"nkv {nkv}")
+
+
+def test_decode_two_query_tokens(eng, orc, rng, cuda):
+    c = llm_case(orc, rng, nq=2, nkv=700, kt=Q8_0, vt=Q4_0, max_seq=1024)
+    run_case(eng, orc, c, what="nq 2")
+
+
+# ------------------------------------------------------------------------------------------
+# prefill with the reference's causal mask (src/cosyvoice-llm.cpp:20-29, 101-108)
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("nq,nkv,kt,vt", [(256, 256, F16, F16), (256, 768, F16, F16), (37, 100, Q8_0, Q4_0),
+                                          (3, 60, F16, F16), (256, 512, Q8_0, Q8_0)])
+def test_prefill_causal(eng, orc, rng, nq, nkv, kt, vt, cuda):
+    mask = orc.causal_mask(nq, nkv)
+    c = llm_case(orc, rng, nq=nq, nkv=nkv, kt=kt, vt=vt, max_seq=nkv + 16, mask=mask, qscale=0.5, kvscale=0.5)
+    run_case(eng, orc, c, what=f"prefill {nq}x{nkv}")
+
+
+def test_mask_rows_wider_than_nkv_and_all_masked_row(eng, orc, rng, cuda):
+    nq, nkv = 5, 70
+    mask = np.zeros((nq + 3, nkv + 9), dtype=np.uint16)  # padded mask: only [:nq, :nkv] is read
+    mask[:, nkv:] = 0x7C00  # +inf beyond n_kv would poison the result if read
+    mask[2, :] = 0xFC00     # a row with every key masked -> 0
+    mask[3, ::2] = 0xFC00
+    c = llm_case(orc, rng, nq=nq, nkv=nkv, kt=Q8_0, vt=Q4_1, mask=mask, max_seq=80)
+    (_, _), got, _ = run_case(eng, orc, c, what="padded mask")
+    assert np.all(got[0, 2] == 0)
+
+
+def test_mask_broadcast_over_heads_and_batch(eng, orc, rng, cuda):
+    nq, nkv, H, B = 4, 90, 14, 2
+    mask = np.where(rng.random((1, 7, nq, nkv)) < 0.3, 0xFC00, 0).astype(np.uint16)  # ne2 = 7 heads, ne3 = 1
+    mask = (mask.view(np.uint16) | np.where(mask == 0, rng.integers(0, 0x3C00, size=mask.shape), 0)).astype(np.uint16)
+    c = llm_case(orc, rng, nq=nq, nkv=nkv, H=H, B=B, kt=F16, vt=Q8_0, mask=mask, max_seq=96)
+    run_case(eng, orc, c, what="mask broadcast")
+
+
+def test_kv_broadcast_over_batch(eng, orc, rng, cuda):
+    c = llm_case(orc, rng, nq=3, nkv=200, B=3, kB=1, kt=Q4_0, vt=Q5_0)
+    run_case(eng, orc, c, what="kv batch broadcast")
+
+
+def test_scale_and_large_logits(eng, orc, rng, cuda):
+    c = llm_case(orc, rng, nq=1, nkv=500, kt=F16, vt=F16, qscale=4.0)
+    run_case(eng, orc, c, scale=0.3, what="large logits")
+
+
+# ------------------------------------------------------------------------------------------
+# DiT (src/cosyvoice-graph.cpp:326-398)
+# ------------------------------------------------------------------------------------------
+def dit_case(orc, rng, *, T, B=2, H=16, Tq=None, mask=None, ttype=F32):
+    Tq = Tq or T
+    c = Case()
+    es = 4 if ttype == F32 else 2
+    npt = np.float32 if ttype == F32 else np.float16
+    for name, n in (("q", Tq), ("k", T), ("v", T)):
+        x = rng.standard_normal((B, n, H * D)).astype(npt)
+        arr = x if ttype == F32 else x.view(np.uint16)
+        row = es * H * D
+        c.add(name, arr, ttype, [D, n, H, B], [es, row, es * D, row * n])
+    c.mask_h = c.mask_d = None
+    if mask is not None:
+        c.add("mask", mask, F16, [mask.shape[1], mask.shape[0], 1, 1],
+              [2, 2 * mask.shape[1], 2 * mask.size, 2 * mask.size])
+    c.out_shape = (B, Tq, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, Tq, B)
+    return c
+
+
+@pytest.mark.parametrize("T", [50, 300, 1500])
+def test_dit_bidirectional_f32(eng, orc, rng, T, cuda):
+    c = dit_case(orc, rng, T=T)
+    run_case(eng, orc, c, what=f"dit T={T}")
+
+
+def test_dit_f16_inputs(eng, orc, rng, cuda):
+    c = dit_case(orc, rng, T=333, ttype=F16)
+    run_case(eng, orc, c, what="dit f16")
+
+
+def test_dit_chunk_mask(eng, orc, rng, cuda):
+    T = 250
+    mask = orc.chunk_mask(T, [50, 100, 150, 200])
+    c = dit_case(orc, rng, T=T, mask=mask)
+    run_case(eng, orc, c, what="dit chunk mask")
+
+
+def test_dit_cut_len_query_subset(eng, orc, rng, cuda):
+    """Last block with cut_len: n_q = T - cut < n_kv = T, one shared mask indexed by local row
+    (src/cosyvoice-graph.cpp:337-343, 453-465)."""
+    T, cut = 180, 60
+    mask = orc.chunk_mask(T, [60, 120])
+    c = dit_case(orc, rng, T=T, Tq=T - cut, mask=mask)
+    run_case(eng, orc, c, what="dit cut_len")
+
+
+@pytest.mark.parametrize("kt,vt", [(F16, F16), (Q8_0, Q4_0)])
+def test_dit_streaming_cache(eng, orc, rng, kt, vt, cuda):
+    """Streaming: a 50-frame chunk over a cached 1000-frame prefix plus itself, cache rows of
+    1024 elements with batch 2 (src/cosyvoice-kv-cache.cpp:104-119, 316-324)."""
+    nq, nkv, max_seq, H, B = 50, 1050, 1200, 16, 2
+    c = Case()
+    q = rng.standard_normal((B, nq, H * D)).astype(np.float32)
+    c.add("q", q, F32, [D, nq, H, B], [4, 4 * H * D, 4 * D, 4 * H * D * nq])
+    for name, t in (("k", kt), ("v", vt)):
+        x = rng.standard_normal((B, max_seq, H * D)).astype(np.float32)
+        b = kv_bytes(orc, t, x)
+        rb = row_bytes(t, H * D)
+        c.add(name, b, t, [D, nkv, H, B], [TYPE_BYTES[t], rb, rb // H, rb * max_seq])
+    c.mask_h = c.mask_d = None
+    c.out_shape = (B, nq, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, nq, B)
+    run_case(eng, orc, c, what="dit stream")
+
+
+# ------------------------------------------------------------------------------------------
+# batched launches (many FA nodes, ragged KV lengths)
+# ------------------------------------------------------------------------------------------
+def test_batch_ragged_matches_single_calls_and_oracle(eng, orc, rng, cuda):
+    lens = [256, 4000, 17, 8192, 1000, 64, 3333, 512]
+    cases = [llm_case(orc, rng, nq=1, nkv=n, kt=Q8_0, vt=Q8_0, max_seq=n + 8) for n in lens]
+    probs = []
+    for c in cases:
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.dst = c.q_d, c.k_d, c.v_d, c.dst_d
+        probs.append(p)
+    wsb = eng.fa_batch_workspace(probs)
+    ws = workspace(wsb)
+    rc, plan = eng.fa_batch_prepare(probs, 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    for _ in range(2):  # a prepared plan can be launched repeatedly
+        assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    for c, n in zip(cases, lens):
+        got = host(c.dst)
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(got, want, what=f"batch nkv {n}")
+        single = empty_f32(*c.out_shape)
+        run_fa(eng, c.q_d, c.k_d, c.v_d, None, cvattn.out_view(single.data_ptr(), D, 14, 1))
+        check_close(host(single), got, max_abs=1e-5, mean_abs=1e-6, what="batch vs single")
+
+
+def test_batch_prefill_with_masks(eng, orc, rng, cuda):
+    cases = []
+    for nkv in (64, 300):
+        mask = orc.causal_mask(16, nkv)
+        cases.append(llm_case(orc, rng, nq=16, nkv=nkv, kt=F16, vt=F16, mask=mask, max_seq=nkv))
+    probs = []
+    for c in cases:
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.mask, p.dst = c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d
+        probs.append(p)
+    ws = workspace(eng.fa_batch_workspace(probs))
+    rc, plan = eng.fa_batch_prepare(probs, 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    for c in cases:
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what="batch prefill")
