@@ -110,6 +110,10 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         len = (n_kv + want - 1) / want;
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
     }
+    // never more splits than the in-kernel merge can weigh
+    const int unit = sh.ks.wsplit ? tstep * sh.ks.nw : tstep;
+    const int min_len = (n_kv + sh.ks.max_splits - 1) / sh.ks.max_splits;
+    if (len < min_len) len = (min_len + unit - 1) / unit * unit;
     *split_len = len;
     *n_splits = n_kv > 0 ? (n_kv + len - 1) / len : 1;
 }

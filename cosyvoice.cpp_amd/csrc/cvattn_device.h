@@ -16,19 +16,32 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint32_t ldg_u32(const uint8_t *p) {
+// Reinterpret a 32-bit word.  The argument is taken by value: with the ROCm 7.2 compiler,
+// __builtin_bit_cast applied directly to an ext_vector element (v[i], i > 0) read element 0.
+__device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
+__device__ __forceinline__ float as_f32(uint32_t x) { return __builtin_bit_cast(float, x); }
+
+// Device memory is read through address-space-1 pointers so the compiler emits global (not
+// flat) loads; flat loads would make every LDS wait also wait for outstanding memory reads.
+typedef const __attribute__((address_space(1))) uint8_t gu8;
+__device__ __forceinline__ gu8 *gptr(const void *p) { return (gu8 *)p; }
+
+// Little-endian loads at any byte alignment (gfx950 global loads accept unaligned addresses).
+__device__ __forceinline__ uint32_t ldg_u32(gu8 *p) {
     uint32_t v;
-    __builtin_memcpy(&v, p, 4);
+    __builtin_memcpy(&v, (const __attribute__((address_space(1))) void *)p, 4);
     return v;
 }
-__device__ __forceinline__ uint32_t ldg_u16(const uint8_t *p) {
-    uint16_t v;
-    __builtin_memcpy(&v, p, 2);
-    return v;
-}
-__device__ __forceinline__ float ldg_half(const uint8_t *p) {
+// 8- and 16-byte loads are typed loads through byte-aligned vector types.  (Copying into a
+// vector local with __builtin_memcpy was miscompiled by the ROCm 7.2 compiler in some kernels:
+// only the first lane of the loaded vector survived.)
+typedef u2 u2_a1 __attribute__((aligned(1)));
+typedef u4 u4_a1 __attribute__((aligned(1)));
+__device__ __forceinline__ u2 ldg_u64(gu8 *p) { return *(const __attribute__((address_space(1))) u2_a1 *)p; }
+__device__ __forceinline__ u4 ldg_u128(gu8 *p) { return *(const __attribute__((address_space(1))) u4_a1 *)p; }
+__device__ __forceinline__ float ldg_half(gu8 *p) {
     _Float16 v;
-    __builtin_memcpy(&v, p, 2);
+    __builtin_memcpy(&v, (const __attribute__((address_space(1))) void *)p, 2);
     return (float)v;
 }
 
@@ -50,47 +63,62 @@ __device__ __forceinline__ uint32_t spread4_hi(uint32_t x) {
 }
 
 // Raw bytes of dims [32*b + 8*c, +8) of one head row, enough to finish unpacking later.
+// Loads only fill integer registers; every conversion happens in raw8_unpack/raw8_scales so
+// that prefetched tiles do not force a wait before the current tile computes.
 struct Raw8 {
     uint32_t w[8]; // f32: 8 words; f16: 4 words; quantized: codes in w[0..1], hi bits in w[2]
-    float d, m;
+    uint32_t dm;   // quantized: fp16 bits of d (low half) and m (high half)
 };
+
+__device__ __forceinline__ uint32_t ldg_u16(gu8 *p) {
+    uint16_t v;
+    __builtin_memcpy(&v, (const __attribute__((address_space(1))) void *)p, 2);
+    return v;
+}
 
 // Issue the loads for dims [32*b + 8*c, +8) of a head row starting at `row`.
 template <int T>
-__device__ __forceinline__ void raw8_load(const uint8_t *row, int b, int c, Raw8 &r) {
+__device__ __forceinline__ void raw8_load(gu8 *row, int b, int c, Raw8 &r) {
     // every field is defined on every path so the struct stays in registers
 #pragma unroll
     for (int i = 0; i < 8; i++) r.w[i] = 0u;
+    r.dm = 0u;
     if constexpr (T == T_F32) {
-        const uint8_t *p = row + (32 * b + 8 * c) * 4;
+        const u4 a = ldg_u128(row + (32 * b + 8 * c) * 4);
+        const u4 e = ldg_u128(row + (32 * b + 8 * c) * 4 + 16);
 #pragma unroll
-        for (int i = 0; i < 8; i++) r.w[i] = ldg_u32(p + 4 * i);
-        r.d = 1.0f;
-        r.m = 0.0f;
-    } else if constexpr (T == T_F16) {
-        const uint8_t *p = row + (32 * b + 8 * c) * 2;
-#pragma unroll
-        for (int i = 0; i < 4; i++) r.w[i] = ldg_u32(p + 4 * i);
-        r.d = 1.0f;
-        r.m = 0.0f;
-    } else {
-        const uint8_t *blk = row + b * type_bytes(T);
-        r.d = ldg_half(blk);
-        r.m = has_min(T) ? ldg_half(blk + 2) : 0.0f;
-        if constexpr (T == T_Q8_0) {
-            const uint8_t *p = blk + 2 + 8 * c;
-            r.w[0] = ldg_u32(p);
-            r.w[1] = ldg_u32(p + 4);
-        } else {
-            constexpr int qs_off = T == T_Q4_0 ? 2 : T == T_Q4_1 ? 4 : T == T_Q5_0 ? 6 : 8;
-            const uint8_t *p = blk + qs_off + 8 * (c & 1);
-            r.w[0] = ldg_u32(p);
-            r.w[1] = ldg_u32(p + 4);
-            if constexpr (T == T_Q5_0 || T == T_Q5_1) {
-                constexpr int qh_off = T == T_Q5_0 ? 2 : 4;
-                r.w[2] = ldg_u32(blk + qh_off);
-            }
+        for (int i = 0; i < 4; i++) {
+            r.w[i] = a[i];
+            r.w[4 + i] = e[i];
         }
+    } else if constexpr (T == T_F16) {
+        const u4 a = ldg_u128(row + (32 * b + 8 * c) * 2);
+#pragma unroll
+        for (int i = 0; i < 4; i++) r.w[i] = a[i];
+    } else {
+        gu8 *blk = row + b * type_bytes(T);
+        if constexpr (has_min(T))
+            r.dm = ldg_u32(blk); // d and m are adjacent
+        else
+            r.dm = ldg_u16(blk);
+        constexpr int qs_off = T == T_Q8_0 ? 2 : T == T_Q4_0 ? 2 : T == T_Q4_1 ? 4 : T == T_Q5_0 ? 6 : 8;
+        const u2 q = ldg_u64(blk + qs_off + (T == T_Q8_0 ? 8 * c : 8 * (c & 1)));
+        r.w[0] = q[0];
+        r.w[1] = q[1];
+        if constexpr (T == T_Q5_0 || T == T_Q5_1) r.w[2] = ldg_u32(blk + (T == T_Q5_0 ? 2 : 4));
+    }
+}
+
+// Block scale d and min m of the loaded block (1 and 0 for f16/f32).
+template <int T>
+__device__ __forceinline__ void raw8_scales(const Raw8 &r, float &d, float &m) {
+    if constexpr (is_quant(T)) {
+        const h2 h = as_h2(r.dm);
+        d = (float)h[0];
+        m = has_min(T) ? (float)h[1] : 0.0f;
+    } else {
+        d = 1.0f;
+        m = 0.0f;
     }
 }
 
@@ -150,6 +178,18 @@ __device__ __forceinline__ float wave_sum16x4(float v) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Device-coherent (agent scope) stores/loads for data one workgroup hands to another.  On
+// gfx950 each XCD has its own L2; these go through to the coherent level (sc1) without the
+// whole-L2 write-back/invalidate a device-scope fence costs.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_agent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until every memory operation this thread issued has completed.
+__device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Workgroup -> unit with consecutive units on one XCD (workgroups are dealt round-robin over
 // the 8 XCDs, so ids w and w+8 share an L2).

@@ -14,6 +14,7 @@ struct FaKernelShape {
     int nw;             // waves per workgroup
     int tstep;          // tokens per staged tile (per wave when wsplit)
     int rows_per_group; // query rows per workgroup
+    int max_splits;     // most token splits one workgroup can merge in-kernel
 };
 FaKernelShape fa_shape(int n_rows);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,

@@ -25,6 +25,7 @@ FaKernelShape fa_shape(int n_rows) {
     s.nw = 4;
     s.tstep = s.wsplit ? FaCfg<4, true>::TSTEP : FaCfg<4, false>::TSTEP;
     s.rows_per_group = s.wsplit ? FaCfg<4, true>::ROWS : FaCfg<4, false>::ROWS;
+    s.max_splits = s.wsplit ? FaCfg<4, true>::MERGE_MAX_SPLITS : FaCfg<4, false>::MERGE_MAX_SPLITS;
     return s;
 }
 

@@ -46,20 +46,18 @@ struct FaCfg {
     static constexpr int THREADS = 64 * NW;
     // staging items handled per thread per step (K and V counted together)
     static constexpr int ITEMS_PER_THREAD = WSPLIT ? 2 : (2 * NITEM) / THREADS;
+    // the K tile buffers double as the split-merge scratch
+    static constexpr int MERGE_MAX_SPLITS = (NSTAGE * TSTEP * KSTR * 2 / 4) / (2 * ROWS);
 };
 
-// Index of the problem owning `key` in a table sorted by `field` (binary search; uniform).
+// Index of the problem owning `key` in a table sorted by `field`: start at the proportional
+// guess (exact when all problems have the same size) and walk; uniform across the workgroup.
 template <int64_t FaProblem::*field>
-__device__ __forceinline__ int find_problem(const FaProblem *table, int n, int64_t key) {
-    int lo = 0, hi = n - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (table[mid].*field <= key)
-            lo = mid;
-        else
-            hi = mid - 1;
-    }
-    return lo;
+__device__ __forceinline__ int find_problem(const FaProblem *table, int n, int64_t key, int64_t total) {
+    int i = total > 0 ? (int)min<int64_t>(n - 1, key * n / total) : 0;
+    while (i > 0 && table[i].*field > key) i--;
+    while (i + 1 < n && table[i + 1].*field <= key) i++;
+    return i;
 }
 
 // Staging item: 4 consecutive tokens x 8 consecutive dims of one 32-dim block.
@@ -71,38 +69,52 @@ __device__ __forceinline__ Item item_of(int it) { return Item{it & 3, (it >> 2) 
 template <int T>
 struct Stage4 {
     Raw8 r[4];
+    uint32_t valid; // bit j: token j of the item is inside the wave's range
 };
 
+// Issue the loads of one staging item.  Rows past `t_lim` read row min(t, n_kv-1) (always in
+// bounds) and are zeroed when stored; nothing here touches the loaded registers, so the loads
+// stay in flight while the current tile computes.
 template <int T>
-__device__ __forceinline__ void stage_load(const uint8_t *base, int64_t nb1, int t0, int t_lim, Item it, Stage4<T> &s) {
+__device__ __forceinline__ void stage_load(gu8 *base, int64_t nb1, int t0, int t_lim, int n_kv, Item it,
+                                           Stage4<T> &s) {
+    s.valid = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int t = t0 + 4 * it.tq + j;
-        if (t < t_lim) {
-            raw8_load<T>(base + (int64_t)t * nb1, it.b, it.c, s.r[j]);
-        } else {
-#pragma unroll
-            for (int w = 0; w < 8; w++) s.r[j].w[w] = 0u;
-            s.r[j].d = 0.0f;
-            s.r[j].m = 0.0f;
-        }
+        raw8_load<T>(base + (int64_t)min(t, n_kv - 1) * nb1, it.b, it.c, s.r[j]);
+        s.valid |= (t < t_lim ? 1u : 0u) << j;
     }
+}
+
+template <int T>
+__device__ __forceinline__ void stage_unpack(const Stage4<T> &s, int j, int c, uint32_t o[4], float &d, float &m) {
+    const bool ok = (s.valid >> j) & 1u;
+    raw8_unpack<T>(s.r[j], c, o);
+    if (!ok) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) o[i] = is_quant(T) ? 0x64006400u : 0u; // code 0 / value 0
+    }
+    raw8_scales<T>(s.r[j], d, m);
+    d = ok ? d : 0.0f;
+    m = ok ? m : 0.0f;
 }
 
 // K tile: natural layout sK[t][dim], scales sKd/sKm[b][t].
 template <int T, int KSTR, int TSTEP>
 __device__ __forceinline__ void stage_store_k(const Stage4<T> &s, Item it, _Float16 *sK, float (*sKd)[TSTEP],
                                               float (*sKm)[TSTEP]) {
+    float d[4], m[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         uint32_t o[4];
-        raw8_unpack<T>(s.r[j], it.c, o);
+        stage_unpack<T>(s, j, it.c, o, d[j], m[j]);
         *(u4 *)&sK[(4 * it.tq + j) * KSTR + 32 * it.b + 8 * it.c] = u4{o[0], o[1], o[2], o[3]};
     }
     if constexpr (is_quant(T)) {
         if (it.c == 0) {
-            *(f4 *)&sKd[it.b][4 * it.tq] = f4{s.r[0].d, s.r[1].d, s.r[2].d, s.r[3].d};
-            if constexpr (has_min(T)) *(f4 *)&sKm[it.b][4 * it.tq] = f4{s.r[0].m, s.r[1].m, s.r[2].m, s.r[3].m};
+            *(f4 *)&sKd[it.b][4 * it.tq] = f4{d[0], d[1], d[2], d[3]};
+            if constexpr (has_min(T)) *(f4 *)&sKm[it.b][4 * it.tq] = f4{m[0], m[1], m[2], m[3]};
         }
     }
 }
@@ -114,13 +126,14 @@ __device__ __forceinline__ void stage_store_v(const Stage4<T> &s, Item it, _Floa
     constexpr float bias = stage_bias<T>();
     const h2 nb2 = {(_Float16)(-bias), (_Float16)(-bias)};
     h2 hv[4][4];
+    float d[4], m[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         uint32_t o[4];
-        raw8_unpack<T>(s.r[j], it.c, o);
+        stage_unpack<T>(s, j, it.c, o, d[j], m[j]);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            h2 x = __builtin_bit_cast(h2, o[i]);
+            h2 x = as_h2(o[i]);
             if constexpr (is_quant(T)) x = x + nb2;
             hv[j][i] = x;
         }
@@ -133,18 +146,43 @@ __device__ __forceinline__ void stage_store_v(const Stage4<T> &s, Item it, _Floa
     }
     if constexpr (is_quant(T)) {
         if (it.c == 0) {
-            *(f4 *)&sVd[it.b][4 * it.tq] = f4{s.r[0].d, s.r[1].d, s.r[2].d, s.r[3].d};
-            if constexpr (has_min(T)) *(f4 *)&sVm[it.b][4 * it.tq] = f4{s.r[0].m, s.r[1].m, s.r[2].m, s.r[3].m};
+            *(f4 *)&sVd[it.b][4 * it.tq] = f4{d[0], d[1], d[2], d[3]};
+            if constexpr (has_min(T)) *(f4 *)&sVm[it.b][4 * it.tq] = f4{m[0], m[1], m[2], m[3]};
         }
     }
 }
 
 // Last-arriving workgroup of a split row group merges all split partials of its rows
-// (prepared batches: no separate combine launch).  Returns true if this workgroup merged.
+// (prepared batches: no separate combine launch).  Three phases so the global loads run in
+// parallel: (1) every split's (m, l) of every row into LDS, (2) one thread per row turns them
+// into normalised split weights, (3) each thread sums its outputs over the splits.
+// `scratch` holds 2 * ROWS * n_splits floats (n_splits <= MERGE_MAX_SPLITS).
 template <int ROWS, int THREADS>
 __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem &P, int bq, int kh, int rg,
-                                             int64_t slot0, int tid) {
-    // slot of (row r, split s) = slot0 + r * n_splits + s
+                                             int64_t slot0, int tid, float *scratch) {
+    const int ns = P.n_splits;
+    float *sm = scratch;             // [ROWS][ns] m, then normalised weights
+    float *sl = scratch + ROWS * ns; // [ROWS][ns] l
+    for (int idx = tid; idx < ROWS * ns; idx += THREADS) {
+        const float *ps = U.partials + (slot0 + idx) * PART_STRIDE; // slot0 + r*ns + s == slot0 + idx
+        sm[idx] = ld_agent(ps + 64);
+        sl[idx] = ld_agent(ps + 65);
+    }
+    __syncthreads();
+    if (tid < ROWS) {
+        float M = -INFINITY;
+        for (int s = 0; s < ns; s++) M = fmaxf(M, sm[tid * ns + s]);
+        float L = 0.0f;
+        if (M != -INFINITY)
+            for (int s = 0; s < ns; s++) {
+                const float w = fast_exp2(sm[tid * ns + s] - M);
+                sm[tid * ns + s] = w;
+                L += sl[tid * ns + s] * w;
+            }
+        const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+        for (int s = 0; s < ns; s++) sm[tid * ns + s] = M != -INFINITY ? sm[tid * ns + s] * inv : 0.0f;
+    }
+    __syncthreads();
     constexpr int PER = ROWS * HEAD / THREADS; // outputs per thread
     static_assert(PER * THREADS == ROWS * HEAD, "merge tiling");
 #pragma unroll
@@ -153,20 +191,12 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
         const int r = idx / HEAD, d = idx % HEAD;
         const int row = rg * ROWS + r;
         if (row >= U.n_rows) continue;
-        const float *part = U.partials + (slot0 + (int64_t)r * P.n_splits) * PART_STRIDE;
-        float M = -INFINITY;
-        for (int s = 0; s < P.n_splits; s++) M = fmaxf(M, part[s * PART_STRIDE + 64]);
-        float L = 0.0f, acc = 0.0f;
-        if (M != -INFINITY) {
-            for (int s = 0; s < P.n_splits; s++) {
-                const float *ps = part + s * PART_STRIDE;
-                const float w = fast_exp2(ps[64] - M);
-                L += ps[65] * w;
-                acc += ps[d] * w;
-            }
-        }
+        const float *part = U.partials + (slot0 + (int64_t)r * ns) * PART_STRIDE + d;
+        float acc = 0.0f;
+#pragma unroll 8
+        for (int s = 0; s < ns; s++) acc += sm[r * ns + s] * ld_agent(part + (int64_t)s * PART_STRIDE);
         const int iq = row / U.G, hq = kh * U.G + row % U.G;
-        P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d] = L > 0.0f ? acc / L : 0.0f;
+        P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d] = acc;
     }
 }
 
@@ -187,7 +217,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
     const int64_t unit = xcd_unit(blockIdx.x, gridDim.x);
     FaProblem P;
     if constexpr (BATCH)
-        P = args.table[find_problem<&FaProblem::unit_begin>(args.table, U.n_problems, unit)];
+        P = args.table[find_problem<&FaProblem::unit_begin>(args.table, U.n_problems, unit, U.total_units)];
     else
         P = args.p0;
 
@@ -214,41 +244,60 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
     const int w_end = WSPLIT ? min(t_end, w_begin + wlen) : t_end;
     const int nsteps = (min(wlen, max(0, t_end - t_begin)) + TSTEP - 1) / TSTEP; // uniform in the workgroup
 
-    const uint8_t *kbase = (const uint8_t *)P.k + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
-    const uint8_t *vbase = (const uint8_t *)P.v + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
+    gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
+    gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
 
     // ---- this lane's query row and its Q operand (B of the S^T MFMA) ----
     const int row = rg * C::ROWS + (WSPLIT ? 0 : wv * 16) + col;
     const bool row_ok = row < U.n_rows;
     const int iq = row_ok ? row / U.G : 0;
     const int hq = kh * U.G + (row_ok ? row % U.G : 0);
-    h8 qop[2];
+    // Q*scale*log2(e) = hi + lo, both fp16: two MFMAs make the QK products fp32-accurate
+    // (lo is zero when Q is f16 and the scale is a power of two, and its MFMA is skipped then).
+    h8 qhi[2], qlo[2];
     float qsum[2];
+    bool need_lo = false;
     {
-        const uint8_t *qp = (const uint8_t *)P.q + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 +
-                            (int64_t)bq * P.q_nb3;
+        gu8 *qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)bq * P.q_nb3;
+        // independent scalar loads, all issued before any use (16-byte vector loads of Q were
+        // miscompiled here by the ROCm 7.2 compiler: only two lanes of each load survived)
+        float x[2][8];
+        if (U.q_f16) { // uniform
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) x[b][j] = ldg_half(qp + 2 * (32 * b + 8 * g + j));
+        } else {
+#pragma unroll
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+                    x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
+        }
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const int d = 32 * b + 8 * g + j;
-                float x = 0.0f;
-                if (row_ok) x = U.q_f16 ? ldg_half(qp + 2 * d) : __builtin_bit_cast(float, ldg_u32(qp + 4 * d));
-                const _Float16 hx = (_Float16)(x * U.scale_log2);
-                qop[b][j] = hx;
-                s += (float)hx;
+                const float xs = row_ok ? x[b][j] * U.scale_log2 : 0.0f;
+                const _Float16 hx = (_Float16)xs;
+                const _Float16 lx = (_Float16)(xs - (float)hx);
+                qhi[b][j] = hx;
+                qlo[b][j] = lx;
+                need_lo |= lx != (_Float16)0.0f;
+                s += (float)hx + (float)lx;
             }
             qsum[b] = wave_sum16x4(s);
         }
     }
+    need_lo = __syncthreads_or(need_lo) != 0;
     constexpr float kbias = stage_bias<KT>();
     const f4 cinit0 = {-kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0]};
     const f4 cinit1 = {-kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1]};
 
-    const uint8_t *mrow = nullptr;
+    gu8 *mrow = nullptr;
     if constexpr (MASK) {
-        mrow = (const uint8_t *)P.mask + (int64_t)iq * P.m_nb1 + (int64_t)(hq % P.m_ne2) * P.m_nb2 +
+        mrow = gptr(P.mask) + (int64_t)iq * P.m_nb1 + (int64_t)(hq % P.m_ne2) * P.m_nb2 +
                (int64_t)(bq % P.m_ne3) * P.m_nb3;
     }
 
@@ -269,8 +318,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
     Stage4<KT> rk;
     Stage4<VT> rv;
     if (nsteps > 0) {
-        if (do_k) stage_load<KT>(kbase, P.k_nb1, w_begin, w_end, itk, rk);
-        if (do_v) stage_load<VT>(vbase, P.v_nb1, w_begin, w_end, itv, rv);
+        if (do_k) stage_load<KT>(kbase, P.k_nb1, w_begin, w_end, P.n_kv, itk, rk);
+        if (do_v) stage_load<VT>(vbase, P.v_nb1, w_begin, w_end, P.n_kv, itv, rv);
     }
 
     for (int step = 0; step < nsteps; step++) {
@@ -279,8 +328,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
         if (do_v) stage_store_v<VT, VSTR, TSTEP>(rv, itv, sV[st], sVd[st], sVm[st]);
         __syncthreads();
         if (step + 1 < nsteps) { // next tile's loads fly while this one computes
-            if (do_k) stage_load<KT>(kbase, P.k_nb1, t0 + TSTEP, w_end, itk, rk);
-            if (do_v) stage_load<VT>(vbase, P.v_nb1, t0 + TSTEP, w_end, itv, rv);
+            if (do_k) stage_load<KT>(kbase, P.k_nb1, t0 + TSTEP, w_end, P.n_kv, itk, rk);
+            if (do_v) stage_load<VT>(vbase, P.v_nb1, t0 + TSTEP, w_end, P.n_kv, itv, rv);
         }
 
         // ---------------- S^T = K Q^T, tile by tile ----------------
@@ -290,8 +339,12 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
         for (int tt = 0; tt < NTILE; tt++) {
             const h8 a0 = *(const h8 *)&cK[(16 * tt + col) * KSTR + 8 * g];
             const h8 a1 = *(const h8 *)&cK[(16 * tt + col) * KSTR + 32 + 8 * g];
-            const f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qop[0], cinit0, 0, 0, 0);
-            const f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qop[1], cinit1, 0, 0, 0);
+            f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
+            f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], cinit1, 0, 0, 0);
+            if (need_lo) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[0], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc1, 0, 0, 0);
+            }
             if constexpr (is_quant(KT)) {
                 const f4 d0 = *(const f4 *)&sKd[st][0][16 * tt + 4 * g];
                 const f4 d1 = *(const f4 *)&sKd[st][1][16 * tt + 4 * g];
@@ -309,26 +362,28 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
 
         // ---------------- mask, bounds, online softmax (base 2) ----------------
         float mx = -INFINITY;
+        const bool full = t0 + TSTEP <= w_end; // uniform: the whole tile is in range
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
             const int tb = t0 + 16 * tt + 4 * g;
             if constexpr (MASK) {
-                if (tb + 3 < w_end) {
-                    const uint8_t *mp = mrow + (int64_t)tb * 2;
-                    const h2 a = __builtin_bit_cast(h2, ldg_u32(mp));
-                    const h2 c2 = __builtin_bit_cast(h2, ldg_u32(mp + 4));
+                if (full) {
+                    const u2 mw = ldg_u64(mrow + (int64_t)tb * 2);
+                    const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
                     s[tt][0] += (float)a[0] * 1.4426950408889634f;
                     s[tt][1] += (float)a[1] * 1.4426950408889634f;
                     s[tt][2] += (float)c2[0] * 1.4426950408889634f;
                     s[tt][3] += (float)c2[1] * 1.4426950408889634f;
                 } else {
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        s[tt][j] = tb + j < w_end ? s[tt][j] + ldg_half(mrow + (int64_t)(tb + j) * 2) * 1.4426950408889634f
-                                                  : -INFINITY;
+                    for (int j = 0; j < 4; j++) {
+                        const int t = tb + j;
+                        const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
+                        s[tt][j] = t < w_end ? s[tt][j] + mv * 1.4426950408889634f : -INFINITY;
+                    }
                 }
             } else {
-                if (tb + 3 >= w_end) {
+                if (!full) {
 #pragma unroll
                     for (int j = 0; j < 4; j++)
                         if (tb + j >= w_end) s[tt][j] = -INFINITY;
@@ -442,10 +497,19 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                 *(f4 *)&out[16 * wv + 4 * g] = o * inv;
             } else {
                 float *out = U.partials + (slot0 + (int64_t)col * P.n_splits + split) * PART_STRIDE;
-                *(f4 *)&out[16 * wv + 4 * g] = o;
-                if (wv == 0 && g == 0) {
-                    out[64] = M;
-                    out[65] = L;
+                if constexpr (BATCH) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++) st_agent(&out[16 * wv + 4 * g + j], o[j]);
+                    if (wv == 0 && g == 0) {
+                        st_agent(&out[64], M);
+                        st_agent(&out[65], L);
+                    }
+                } else {
+                    *(f4 *)&out[16 * wv + 4 * g] = o;
+                    if (wv == 0 && g == 0) {
+                        out[64] = M;
+                        out[65] = L;
+                    }
                 }
             }
         }
@@ -458,11 +522,22 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                 for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i] * inv;
             } else {
                 float *o = U.partials + (slot0 + (int64_t)(row - rg * C::ROWS) * P.n_splits + split) * PART_STRIDE;
+                if constexpr (BATCH) {
 #pragma unroll
-                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i];
-                if (g == 0) {
-                    o[64] = m_run;
-                    o[65] = l_run;
+                    for (int i = 0; i < 4; i++)
+#pragma unroll
+                        for (int j = 0; j < 4; j++) st_agent(&o[16 * i + 4 * g + j], oacc[i][j]);
+                    if (g == 0) {
+                        st_agent(&o[64], m_run);
+                        st_agent(&o[65], l_run);
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i];
+                    if (g == 0) {
+                        o[64] = m_run;
+                        o[65] = l_run;
+                    }
                 }
             }
         }
@@ -471,21 +546,21 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
     // prepared batches: the last split of a row group to arrive merges the partials
     if constexpr (BATCH) {
         if (P.n_splits > 1) {
+            // partials were stored with agent-scope stores; once they have completed, the
+            // arrival count publishes them (no device-wide fence, which would flush the L2)
             __shared__ uint32_t s_last;
-            __threadfence();
+            wait_memory();
             __syncthreads();
             if (tid == 0) {
                 uint32_t *cnt = U.counters + P.cnt_begin + ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
-                const uint32_t prev = atomicAdd(cnt, 1u);
+                const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const bool last = prev == (uint32_t)(P.n_splits - 1);
-                if (last) atomicExch(cnt, 0u); // leave the counter zeroed for the next launch
+                // the last arrival leaves the counter zeroed for the next launch
+                if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 s_last = last ? 1u : 0u;
             }
             __syncthreads();
-            if (s_last) {
-                __threadfence();
-                merge_splits<C::ROWS, C::THREADS>(U, P, bq, kh, rg, slot0, tid);
-            }
+            if (s_last) merge_splits<C::ROWS, C::THREADS>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
         }
     }
 }
@@ -497,7 +572,7 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
     const int64_t row = blockIdx.x;
     FaProblem P;
     if constexpr (BATCH)
-        P = args.table[find_problem<&FaProblem::row_begin>(args.table, U.n_problems, row)];
+        P = args.table[find_problem<&FaProblem::row_begin>(args.table, U.n_problems, row, U.total_rows)];
     else
         P = args.p0;
     if (P.n_splits == 1) return;
@@ -512,11 +587,14 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
     const int64_t slot0 = P.part_begin + ((((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * ROWS + rr) * P.n_splits;
     const float *part = U.partials + slot0 * PART_STRIDE;
     const int d = threadIdx.x;
+    const int ns = P.n_splits;
     float M = -INFINITY;
-    for (int s = 0; s < P.n_splits; s++) M = fmaxf(M, part[s * PART_STRIDE + 64]);
+#pragma unroll 8
+    for (int s = 0; s < ns; s++) M = fmaxf(M, part[s * PART_STRIDE + 64]);
     float L = 0.0f, acc = 0.0f;
     if (M != -INFINITY) {
-        for (int s = 0; s < P.n_splits; s++) {
+#pragma unroll 8
+        for (int s = 0; s < ns; s++) {
             const float *ps = part + s * PART_STRIDE;
             const float w = fast_exp2(ps[64] - M);
             L += ps[65] * w;

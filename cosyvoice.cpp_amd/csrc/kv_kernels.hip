@@ -17,20 +17,22 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *src, float 
     const int c = (int)(gid & 3);
     const int64_t row_bytes = T == T_F16 ? 64 : type_bytes(T);
     Raw8 r;
-    raw8_load<T>(src + blk * row_bytes, 0, c, r);
+    raw8_load<T>(gptr(src) + blk * row_bytes, 0, c, r);
     uint32_t o[4];
     raw8_unpack<T>(r, c, o);
+    float rd, rm;
+    raw8_scales<T>(r, rd, rm);
     constexpr float bias = stage_bias<T>();
     float y[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const h2 h = __builtin_bit_cast(h2, o[i]);
+        const h2 h = as_h2(o[i]);
 #pragma unroll
         for (int s = 0; s < 2; s++) {
             if constexpr (is_quant(T)) {
                 // (code)*d is exact in fp32; only "+ m" rounds, as in ggml's dequantizers
                 const float code = (float)h[s] - bias;
-                y[2 * i + s] = has_min(T) ? code * r.d + r.m : code * r.d;
+                y[2 * i + s] = has_min(T) ? code * rd + rm : code * rd;
             } else {
                 y[2 * i + s] = (float)h[s];
             }
@@ -55,9 +57,14 @@ __global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16 *src, fl
 // ggml quantize_row_*_ref, one 32-element block per thread.  Contraction is disabled so each
 // multiply/add rounds exactly like the reference C (x*id then +8.5f are separate roundings).
 // ------------------------------------------------------------------------------------------
+// fp32 -> fp16 (round to nearest even).  The sign bit is taken from the fp32 value: the
+// backend may fold "x * c -> fp16" into an fma with a +0 addend, which turns -0 into +0
+// (q4_0/q5_0 blocks of zeros have d = 0 / -8 = -0, and ggml stores that sign).
 __device__ __forceinline__ void st_half(uint8_t *p, float f) {
     const _Float16 h = (_Float16)f;
-    __builtin_memcpy(p, &h, 2);
+    uint16_t bits = __builtin_bit_cast(uint16_t, h);
+    bits = (uint16_t)((bits & 0x7fffu) | ((__builtin_bit_cast(uint32_t, f) >> 16) & 0x8000u));
+    __builtin_memcpy(p, &bits, 2);
 }
 
 template <int T>

@@ -67,6 +67,15 @@ def test_quantize_single_spike_known_bytes(orc, j):
     assert list(b[8:]) == qs
 
 
+def test_zero_block_scales_keep_ieee_sign(orc):
+    """0 / -8 and 0 / -16 are -0.0 in IEEE arithmetic, so all-zero q4_0/q5_0 blocks store d = -0."""
+    x = np.zeros(32, dtype=np.float32)
+    assert list(orc.quantize_flat(Q4_0, x)[:2]) == [0x00, 0x80]
+    assert list(orc.quantize_flat(Q5_0, x)[:2]) == [0x00, 0x80]
+    assert list(orc.quantize_flat(Q8_0, x)[:2]) == [0x00, 0x00]  # 0 / 127 = +0
+    assert list(orc.quantize_flat(Q4_1, x)[:4]) == [0, 0, 0, 0]
+
+
 def test_quantize_negative_spike_and_sign_of_d(orc):
     x = np.zeros(32, dtype=np.float32)
     x[3] = -2.0
