@@ -71,7 +71,10 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     sh->B = (int)q->ne[3];
     sh->n_kv = (int)k->ne[1];
     sh->n_rows = sh->n_q * sh->G;
-    sh->ks = fa_shape(sh->n_rows);
+    // 32-bit buffer offsets cover each K/V head view (decode kernel)
+    const int64_t lim31 = ((int64_t)1 << 31) - 1;
+    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] < lim31 && (int64_t)v->ne[1] * (int64_t)v->nb[1] < lim31;
+    sh->ks = fa_shape(sh->n_rows, small);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
     return CVATTN_OK;
 }
@@ -334,6 +337,12 @@ CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n,
     fill_uniform(bp.args.u, sh, problems[0].q.type, scale);
     bp.args.u.n_problems = n;
     bp.args.u.total_units = lay.units;
+    {
+        const int64_t u0 = n > 1 ? table[1].unit_begin - table[0].unit_begin : lay.units;
+        bool uniform = u0 > 0;
+        for (int i = 0; i < n && uniform; i++) uniform = table[i].unit_begin == (int64_t)i * u0;
+        bp.args.u.units_per_problem = uniform && (int64_t)n * u0 == lay.units ? u0 : 0;
+    }
     bp.args.u.total_rows = lay.rows;
     bp.args.u.counters = (uint32_t *)((char *)ws + lay.table_bytes);
     bp.args.u.partials = (float *)((char *)ws + lay.table_bytes + lay.counter_bytes);

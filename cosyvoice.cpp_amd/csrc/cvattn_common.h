@@ -76,6 +76,7 @@ struct FaUniform {
     int32_t q_f16;       // Q element type: 0 f32, 1 f16
     int32_t n_problems;
     float scale_log2;    // scale * log2(e)
+    int64_t units_per_problem; // > 0 when every problem has this many workgroup units
     int64_t total_units;
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)
     float *partials;     // workspace: split partial (m, l, O[64]) per row slot

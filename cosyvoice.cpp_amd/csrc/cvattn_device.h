@@ -20,6 +20,7 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 // __builtin_bit_cast applied directly to an ext_vector element (v[i], i > 0) read element 0.
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 __device__ __forceinline__ float as_f32(uint32_t x) { return __builtin_bit_cast(float, x); }
+__device__ __forceinline__ h8 as_h8(u4 x) { return __builtin_bit_cast(h8, x); }
 
 // Device memory is read through address-space-1 pointers so the compiler emits global (not
 // flat) loads; flat loads would make every LDS wait also wait for outstanding memory reads.
@@ -62,12 +63,17 @@ __device__ __forceinline__ uint32_t spread4_hi(uint32_t x) {
     return (((x & 0xfu) * 0x00204081u) & 0x01010101u) << 4;
 }
 
-// Raw bytes of dims [32*b + 8*c, +8) of one head row, enough to finish unpacking later.
-// Loads only fill integer registers; every conversion happens in raw8_unpack/raw8_scales so
-// that prefetched tiles do not force a wait before the current tile computes.
+// Raw words of dims [32*b + 8*c, +8) of one head row, sized for the type so prefetched tiles
+// cost only the registers they need.  Loads only fill integer registers; every conversion
+// happens in raw8_unpack/raw8_scales so prefetched tiles do not force a wait.
+template <int T>
+__host__ __device__ constexpr int raw_words() {
+    return T == T_F32 ? 8 : T == T_F16 ? 4 : (T == T_Q5_0 || T == T_Q5_1) ? 3 : 2;
+}
+template <int T>
 struct Raw8 {
-    uint32_t w[8]; // f32: 8 words; f16: 4 words; quantized: codes in w[0..1], hi bits in w[2]
-    uint32_t dm;   // quantized: fp16 bits of d (low half) and m (high half)
+    uint32_t w[raw_words<T>()];
+    uint32_t dm; // quantized: fp16 bits of d (low half) and m (high half)
 };
 
 __device__ __forceinline__ uint32_t ldg_u16(gu8 *p) {
@@ -78,10 +84,7 @@ __device__ __forceinline__ uint32_t ldg_u16(gu8 *p) {
 
 // Issue the loads for dims [32*b + 8*c, +8) of a head row starting at `row`.
 template <int T>
-__device__ __forceinline__ void raw8_load(gu8 *row, int b, int c, Raw8 &r) {
-    // every field is defined on every path so the struct stays in registers
-#pragma unroll
-    for (int i = 0; i < 8; i++) r.w[i] = 0u;
+__device__ __forceinline__ void raw8_load(gu8 *row, int b, int c, Raw8<T> &r) {
     r.dm = 0u;
     if constexpr (T == T_F32) {
         const u4 a = ldg_u128(row + (32 * b + 8 * c) * 4);
@@ -111,7 +114,7 @@ __device__ __forceinline__ void raw8_load(gu8 *row, int b, int c, Raw8 &r) {
 
 // Block scale d and min m of the loaded block (1 and 0 for f16/f32).
 template <int T>
-__device__ __forceinline__ void raw8_scales(const Raw8 &r, float &d, float &m) {
+__device__ __forceinline__ void raw8_scales(const Raw8<T> &r, float &d, float &m) {
     if constexpr (is_quant(T)) {
         const h2 h = as_h2(r.dm);
         d = (float)h[0];
@@ -125,14 +128,11 @@ __device__ __forceinline__ void raw8_scales(const Raw8 &r, float &d, float &m) {
 // Unpack to 8 fp16 in natural dim order (4 dwords).  Quantized types give 1024 + u where u is
 // the unsigned code (true code = u - code_off(T)); f16 gives the values, f32 rounds to fp16.
 template <int T>
-__device__ __forceinline__ void raw8_unpack(const Raw8 &r, int c, uint32_t o[4]) {
+__device__ __forceinline__ void raw8_unpack(const Raw8<T> &r, int c, uint32_t o[4]) {
     if constexpr (T == T_F32) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            float x0, x1;
-            __builtin_memcpy(&x0, &r.w[2 * i], 4);
-            __builtin_memcpy(&x1, &r.w[2 * i + 1], 4);
-            h2 h = {(_Float16)x0, (_Float16)x1};
+            h2 h = {(_Float16)as_f32(r.w[2 * i]), (_Float16)as_f32(r.w[2 * i + 1])};
             o[i] = __builtin_bit_cast(uint32_t, h);
         }
     } else if constexpr (T == T_F16) {

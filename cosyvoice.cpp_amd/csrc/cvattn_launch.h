@@ -16,7 +16,7 @@ struct FaKernelShape {
     int rows_per_group; // query rows per workgroup
     int max_splits;     // most token splits one workgroup can merge in-kernel
 };
-FaKernelShape fa_shape(int n_rows);
+FaKernelShape fa_shape(int n_rows, bool small_views);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
 

@@ -19,13 +19,15 @@ static int type_index(int t) {
     }
 }
 
-FaKernelShape fa_shape(int n_rows) {
+FaKernelShape fa_shape(int n_rows, bool small_views) {
     FaKernelShape s;
-    s.wsplit = n_rows <= 16;
+    // decode-shaped kernel (fa_decode.h): <= 16 rows, and K/V views addressable with 32-bit
+    // buffer offsets; everything else runs the row-tiled kernel
+    s.wsplit = n_rows <= 16 && small_views;
     s.nw = 4;
-    s.tstep = s.wsplit ? FaCfg<4, true>::TSTEP : FaCfg<4, false>::TSTEP;
-    s.rows_per_group = s.wsplit ? FaCfg<4, true>::ROWS : FaCfg<4, false>::ROWS;
-    s.max_splits = s.wsplit ? FaCfg<4, true>::MERGE_MAX_SPLITS : FaCfg<4, false>::MERGE_MAX_SPLITS;
+    s.tstep = s.wsplit ? 64 : FaCfg<4, false>::TSTEP;
+    s.rows_per_group = s.wsplit ? 16 : FaCfg<4, false>::ROWS;
+    s.max_splits = s.wsplit ? (1 << 20) : FaCfg<4, false>::MERGE_MAX_SPLITS;
     return s;
 }
 

@@ -68,7 +68,7 @@ __device__ __forceinline__ Item item_of(int it) { return Item{it & 3, (it >> 2) 
 
 template <int T>
 struct Stage4 {
-    Raw8 r[4];
+    Raw8<T> r[4];
     uint32_t valid; // bit j: token j of the item is inside the wave's range
 };
 

@@ -16,7 +16,7 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *src, float 
     if (blk >= n_groups) return;
     const int c = (int)(gid & 3);
     const int64_t row_bytes = T == T_F16 ? 64 : type_bytes(T);
-    Raw8 r;
+    Raw8<T> r;
     raw8_load<T>(gptr(src) + blk * row_bytes, 0, c, r);
     uint32_t o[4];
     raw8_unpack<T>(r, c, o);
