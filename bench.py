@@ -196,6 +196,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=260)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-dit", action="store_true", help="skip the DiT leg")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run 256 MiB device copies (reference kernels for the HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this attention path has "
@@ -206,8 +208,20 @@ def main():
 
     import cvattn
 
-    lib = cvattn.lib()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        n = 256 * 2**20 // 4
+        a = torch.randn(n, device=dev)
+        b = torch.empty_like(a)
+        for _ in range(10):
+            b.copy_(a)  # the runtime's blit kernel
+        for _ in range(10):
+            torch.neg(a, out=b)  # an elementwise kernel: plain vector loads and stores
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                          "launches": {"copyBuffer": 10, "neg": 10}}))
+        return
+    lib = cvattn.lib()
     kt, vt = cvattn.Q8_0, cvattn.Q4_0
     per_layer = decode_bytes_per_layer(34, 18)
     per_copy = L * (MAX_SEQ * (cvattn.row_bytes(kt, HKV * D) + cvattn.row_bytes(vt, HKV * D)))
@@ -261,7 +275,7 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q8_0/q4_0 KV, f16 MFMA, f32 accumulate",
+        "dtype": "f16 MFMA + f32",
         "data": "synthetic: seeded N(0,1) K/V quantized on device with ggml's reference quantizers, N(0,1) Q",
         "config": {
             "workload": "decode attention, 24 layers x 1 token, batch 1, 14/2 heads, head_dim 64, "

@@ -169,7 +169,13 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
     u.n_rowgroups = sh.n_rowgroups;
     u.q_f16 = q_type == T_F16 ? 1 : 0;
     u.scale_log2 = scale * 1.4426950408889634f;
+    u.div_hkv = make_fastdiv((uint32_t)sh.H_kv);
+    u.div_rowgroups = make_fastdiv((uint32_t)sh.n_rowgroups);
+    u.div_upp = make_fastdiv(1);
 }
+
+// Workgroup units of a launch are decomposed with 32-bit arithmetic.
+constexpr int64_t kMaxUnits = ((int64_t)1 << 31) - 1;
 
 int64_t slots_per_split(const FaShape &sh) {
     return (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * sh.ks.rows_per_group;
@@ -240,9 +246,11 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
     fill_uniform(a.u, pl.sh, q->type, scale);
     fill_problem(a.p0, q, k, v, mask, dst, pl.sh);
     a.p0.n_splits = pl.n_splits;
+    a.p0.div_splits = make_fastdiv((uint32_t)pl.n_splits);
     a.p0.split_len = pl.split_len;
     a.u.n_problems = 1;
     a.u.total_units = (int64_t)pl.sh.B * pl.sh.H_kv * pl.sh.n_rowgroups * pl.n_splits;
+    if (a.u.total_units > kMaxUnits) return CVATTN_ERR_UNSUPPORTED;
     a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
     a.u.partials = (float *)ws;
     const bool has_mask = mask && mask->data;
@@ -288,6 +296,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         FaProblem fp;
         fill_problem(fp, &p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &p.dst, sh);
         fp.n_splits = ns;
+        fp.div_splits = make_fastdiv((uint32_t)ns);
         fp.split_len = sl;
         fp.unit_begin = unit;
         fp.part_begin = part;
@@ -305,6 +314,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
     lay->table_bytes = align_up(sizeof(FaProblem) * (size_t)n, kAlign);
     lay->counter_bytes = align_up(sizeof(uint32_t) * (size_t)cnt, kAlign);
     lay->total_bytes = lay->table_bytes + lay->counter_bytes + (size_t)part * PART_STRIDE * sizeof(float);
+    if (unit > kMaxUnits) return CVATTN_ERR_UNSUPPORTED;
     lay->units = unit;
     lay->rows = row;
     return CVATTN_OK;
@@ -342,6 +352,7 @@ CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n,
         bool uniform = u0 > 0;
         for (int i = 0; i < n && uniform; i++) uniform = table[i].unit_begin == (int64_t)i * u0;
         bp.args.u.units_per_problem = uniform && (int64_t)n * u0 == lay.units ? u0 : 0;
+        if (bp.args.u.units_per_problem > 0) bp.args.u.div_upp = make_fastdiv((uint32_t)u0);
     }
     bp.args.u.total_rows = lay.rows;
     bp.args.u.counters = (uint32_t *)((char *)ws + lay.table_bytes);

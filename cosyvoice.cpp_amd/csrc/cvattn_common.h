@@ -46,6 +46,24 @@ __host__ __device__ constexpr int code_off(int t) {
 __host__ __device__ constexpr bool has_min(int t) { return t == T_Q4_1 || t == T_Q5_1; }
 __host__ __device__ constexpr bool is_quant(int t) { return type_block(t) == QK; }
 
+// Division by a runtime constant d >= 1 for 0 <= n < 2^31: q = (n * mul) >> shift with
+// shift = 31 + ceil(log2 d) and mul = ceil(2^shift / d) < 2^32 (round-up method; the error term
+// n*(mul*d - 2^shift) / (d*2^shift) < 1/d never carries the quotient over).  Workgroup indices
+// are decomposed with these on the scalar unit instead of 64-bit division routines.
+struct FastDiv {
+    uint32_t mul, shift, d;
+};
+inline FastDiv make_fastdiv(uint32_t d) {
+    uint32_t l = 0;
+    while (l < 31 && (1u << l) < d) l++;
+    const uint32_t shift = 31 + l;
+    const uint64_t mul = (((uint64_t)1 << shift) + d - 1) / d;
+    return FastDiv{(uint32_t)mul, shift, d};
+}
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, FastDiv f) {
+    return (uint32_t)(((uint64_t)n * f.mul) >> f.shift);
+}
+
 // One attention problem as the kernels see it (strides in bytes; nb0 is implied by the type).
 struct FaProblem {
     const void *q;
@@ -66,6 +84,7 @@ struct FaProblem {
     int64_t part_begin;   // first partial slot (rows) of this problem in the workspace
     int64_t row_begin;    // first output row (b, i, h) of this problem (combine indexing)
     int64_t cnt_begin;    // first split-arrival counter of this problem (prepared batches)
+    FastDiv div_splits;   // n_splits
 };
 
 // Parameters shared by every problem of one launch.
@@ -76,6 +95,7 @@ struct FaUniform {
     int32_t q_f16;       // Q element type: 0 f32, 1 f16
     int32_t n_problems;
     float scale_log2;    // scale * log2(e)
+    FastDiv div_hkv, div_rowgroups, div_upp; // H_kv, n_rowgroups, units_per_problem
     int64_t units_per_problem; // > 0 when every problem has this many workgroup units
     int64_t total_units;
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)

@@ -21,6 +21,9 @@ typedef uint32_t u2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2 as_h2(uint32_t x) { return __builtin_bit_cast(h2, x); }
 __device__ __forceinline__ float as_f32(uint32_t x) { return __builtin_bit_cast(float, x); }
 __device__ __forceinline__ h8 as_h8(u4 x) { return __builtin_bit_cast(h8, x); }
+__device__ __forceinline__ uint32_t as_u32(float x) { return __builtin_bit_cast(uint32_t, x); }
+__device__ __forceinline__ u4 as_u4(f4 x) { return __builtin_bit_cast(u4, x); }
+__device__ __forceinline__ f4 as_f4(u4 x) { return __builtin_bit_cast(f4, x); }
 
 // Device memory is read through address-space-1 pointers so the compiler emits global (not
 // flat) loads; flat loads would make every LDS wait also wait for outstanding memory reads.
@@ -193,8 +196,8 @@ __device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Workgroup -> unit with consecutive units on one XCD (workgroups are dealt round-robin over
 // the 8 XCDs, so ids w and w+8 share an L2).
-__device__ __forceinline__ int64_t xcd_unit(int64_t w, int64_t n) {
-    const int64_t x = w & 7, i = w >> 3, q = n >> 3, r = n & 7;
+__device__ __forceinline__ uint32_t xcd_unit(uint32_t w, uint32_t n) {
+    const uint32_t x = w & 7, i = w >> 3, q = n >> 3, r = n & 7;
     return x * q + (x < r ? x : r) + i;
 }
 

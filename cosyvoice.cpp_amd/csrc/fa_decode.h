@@ -27,6 +27,7 @@ constexpr int DEC_NW = 4;      // waves per workgroup
 constexpr int DEC_TS = 64;     // tokens per wave step
 constexpr int DEC_VSTR = 68;   // halfs per staged V^T row (64 tokens + pad)
 constexpr float DEC_RESCALE_LOG2 = 8.0f;
+constexpr int DEC_MERGE_CHUNK = 16; // split partials loaded together by the merging workgroup
 
 // Buffer resource over [base, base + bytes); loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(gu8 *base, int64_t bytes) {
@@ -110,24 +111,11 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     __shared__ uint32_t s_last;
 
     const FaUniform &U = args.u;
-    const int64_t unit = xcd_unit(blockIdx.x, gridDim.x);
     FaProblem P;
-    if constexpr (BATCH) {
-        const int pi = U.units_per_problem > 0 ? (int)(unit / U.units_per_problem)
-                                               : find_problem<&FaProblem::unit_begin>(args.table, U.n_problems, unit,
-                                                                                     U.total_units);
-        P = args.table[pi];
-    } else {
-        P = args.p0;
-    }
-
-    int64_t ul = unit - P.unit_begin;
-    const int kh = (int)(ul % U.H_kv);
-    ul /= U.H_kv;
-    const int rg = (int)(ul % U.n_rowgroups);
-    ul /= U.n_rowgroups;
-    const int split = (int)(ul % P.n_splits);
-    const int bq = (int)(ul / P.n_splits);
+    // consecutive units (the kv heads of one token range, whose rows share cache lines) run on
+    // one XCD so each line is fetched into one L2 only
+    const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
+    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int col = lane & 15, g = lane >> 4;
@@ -390,8 +378,9 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         for (int j = 0; j < 4; j++) o[j] += xo[(w * 64 + 16 * wv + 4 * g + j) * 16 + col] * f;
     }
     // wave wv now owns dims 16*wv + 4g + j of row `col`
-    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * 16 * P.n_splits;
-    if (P.n_splits == 1) {
+    const int ns = P.n_splits;
+    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * 16 * ns;
+    if (ns == 1) {
         if (row_ok) {
             const float inv = L > 0.0f ? 1.0f / L : 0.0f;
             float *out = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
@@ -399,8 +388,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         return;
     }
-    float *part = U.partials + (slot0 + (int64_t)col * P.n_splits + split) * PART_STRIDE;
     if constexpr (!BATCH) {
+        float *part = U.partials + (slot0 + (int64_t)col * ns + split) * PART_STRIDE;
         if (row_ok) {
             *(f4 *)&part[16 * wv + 4 * g] = o;
             if (wv == 0 && g == 0) {
@@ -410,46 +399,65 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         return;
     } else {
+        // Partials of this (batch, kv head, row group): [16 rows][ns splits][PART_STRIDE floats],
+        // written and read with agent-coherent (sc1) buffer accesses, the form the compiler gives
+        // agent-scope atomic loads and stores, but vectorised and all in flight at once.
+        constexpr int SC1 = 16;
+        const __amdgpu_buffer_rsrc_t rp =
+            make_rsrc((gu8 *)(U.partials + slot0 * PART_STRIDE), (int64_t)16 * ns * PART_STRIDE * 4);
         if (row_ok) {
-#pragma unroll
-            for (int j = 0; j < 4; j++) st_agent(&part[16 * wv + 4 * g + j], o[j]);
-            if (wv == 0 && g == 0) {
-                st_agent(&part[64], M);
-                st_agent(&part[65], L);
-            }
+            const int base = (col * ns + split) * PART_STRIDE * 4;
+            __builtin_amdgcn_raw_buffer_store_b128(as_u4(o), rp, base + (16 * wv + 4 * g) * 4, 0, SC1);
+            if (wv == 0 && g == 0)
+                __builtin_amdgcn_raw_buffer_store_b64(u2{as_u32(M), as_u32(L)}, rp, base + 64 * 4, 0, SC1);
         }
-        // the partials were stored with agent-scope stores; once they have completed, the
-        // arrival count publishes them (a device-wide fence would write back the whole L2)
+        // once the partials have completed, the arrival count publishes them (a device-wide
+        // fence would write back the whole L2)
         wait_memory();
         __syncthreads();
         if (tid == 0) {
             uint32_t *cnt = U.counters + P.cnt_begin + ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
             const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            const bool last = prev == (uint32_t)(P.n_splits - 1);
+            const bool last = prev == (uint32_t)(ns - 1);
             if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             s_last = last ? 1u : 0u;
         }
         __syncthreads();
         if (!s_last) return;
-        // last arrival: online merge of every split of its 16 rows; thread = (row, 4 dims)
+        // last arrival: merge every split of its 16 rows; thread = (row, 4 dims); the loads of
+        // up to DEC_MERGE_CHUNK splits are issued together
         const int r = tid >> 4, d0 = (tid & 15) * 4;
         const int rrow = rg * 16 + r;
         if (rrow >= U.n_rows) return;
-        const float *pr = U.partials + (slot0 + (int64_t)r * P.n_splits) * PART_STRIDE;
         float Mm = -INFINITY, Ll = 0.0f;
         f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll 8
-        for (int sp = 0; sp < P.n_splits; sp++) {
-            const float *ps = pr + (int64_t)sp * PART_STRIDE;
-            const float m = ld_agent(ps + 64), l = ld_agent(ps + 65);
-            const f4 ov = {ld_agent(ps + d0), ld_agent(ps + d0 + 1), ld_agent(ps + d0 + 2), ld_agent(ps + d0 + 3)};
-            const float mn = fmaxf(Mm, m);
-            if (mn != -INFINITY) {
-                const float a = fast_exp2(Mm - mn), bb = fast_exp2(m - mn);
-                Ll = Ll * a + l * bb;
-                acc = acc * a + ov * bb;
-                Mm = mn;
+        for (int c0 = 0; c0 < ns; c0 += DEC_MERGE_CHUNK) {
+            u2 ml[DEC_MERGE_CHUNK];
+            u4 ov[DEC_MERGE_CHUNK];
+#pragma unroll
+            for (int j = 0; j < DEC_MERGE_CHUNK; j++) {
+                const int sp = min(c0 + j, ns - 1);
+                const int base = (r * ns + sp) * PART_STRIDE * 4;
+                ml[j] = __builtin_amdgcn_raw_buffer_load_b64(rp, base + 64 * 4, 0, SC1);
+                ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, base + d0 * 4, 0, SC1);
             }
+            float cm = Mm;
+#pragma unroll
+            for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+                if (c0 + j < ns) cm = fmaxf(cm, as_f32(ml[j][0]));
+            if (cm == -INFINITY) continue; // every row of these splits is fully masked so far
+            const float a = fast_exp2(Mm - cm);
+            Ll *= a;
+            acc *= a;
+#pragma unroll
+            for (int j = 0; j < DEC_MERGE_CHUNK; j++) {
+                if (c0 + j < ns) {
+                    const float f = fast_exp2(as_f32(ml[j][0]) - cm);
+                    Ll += as_f32(ml[j][1]) * f;
+                    acc += as_f4(ov[j]) * f;
+                }
+            }
+            Mm = cm;
         }
         const float inv = Ll > 0.0f ? 1.0f / Ll : 0.0f;
         const int riq = rrow / U.G, rhq = kh * U.G + rrow % U.G;

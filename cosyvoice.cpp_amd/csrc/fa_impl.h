@@ -60,6 +60,51 @@ __device__ __forceinline__ int find_problem(const FaProblem *table, int n, int64
     return i;
 }
 
+// Problem of workgroup unit `unit` in a table whose unit_begin values ascend: each lane of the
+// wave compares one entry, so 64 problems cost one round trip.  Uniform across the workgroup.
+__device__ __forceinline__ int find_problem_wave(const FaProblem *table, int n, uint32_t unit) {
+    int cnt = 0;
+    for (int c0 = 0; c0 < n; c0 += 64) {
+        const int i = c0 + (int)(threadIdx.x & 63);
+        const bool le = i < n && table[i].unit_begin <= (int64_t)unit;
+        cnt += __popcll(__builtin_amdgcn_ballot_w64(le));
+    }
+    return cnt - 1;
+}
+
+// Position of a workgroup unit inside its problem: unit = ((bq*n_splits + split)*H_kv + kh)*
+// n_rowgroups + rg, counted from the problem's unit_begin.  Row groups are innermost so that the
+// units of one XCD (see xcd_unit) share the K/V of few heads in that XCD's L2.
+struct UnitPos {
+    int kh, rg, split, bq;
+};
+template <bool BATCH>
+__device__ __forceinline__ UnitPos locate_unit(const FaArgs &args, uint32_t unit, FaProblem &P) {
+    const FaUniform &U = args.u;
+    uint32_t ul = unit;
+    if (!BATCH || U.n_problems == 1) {
+        P = args.p0;
+    } else if (U.units_per_problem > 0) {
+        const uint32_t pi = fdiv(unit, U.div_upp);
+        P = args.table[pi];
+        ul = unit - pi * (uint32_t)U.units_per_problem;
+    } else {
+        P = args.table[find_problem_wave(args.table, U.n_problems, unit)];
+        ul = unit - (uint32_t)P.unit_begin;
+    }
+    UnitPos r;
+    uint32_t t = fdiv(ul, U.div_rowgroups);
+    r.rg = (int)(ul - t * (uint32_t)U.n_rowgroups);
+    ul = t;
+    t = fdiv(ul, U.div_hkv);
+    r.kh = (int)(ul - t * (uint32_t)U.H_kv);
+    ul = t;
+    t = fdiv(ul, P.div_splits);
+    r.split = (int)(ul - t * (uint32_t)P.n_splits);
+    r.bq = (int)t;
+    return r;
+}
+
 // Staging item: 4 consecutive tokens x 8 consecutive dims of one 32-dim block.
 struct Item {
     int c, b, tq;
@@ -214,20 +259,9 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
     __shared__ __attribute__((aligned(16))) float sVm[NSTAGE][2][TSTEP];
 
     const FaUniform &U = args.u;
-    const int64_t unit = xcd_unit(blockIdx.x, gridDim.x);
     FaProblem P;
-    if constexpr (BATCH)
-        P = args.table[find_problem<&FaProblem::unit_begin>(args.table, U.n_problems, unit, U.total_units)];
-    else
-        P = args.p0;
-
-    int64_t ul = unit - P.unit_begin;
-    const int kh = (int)(ul % U.H_kv);
-    ul /= U.H_kv;
-    const int rg = (int)(ul % U.n_rowgroups);
-    ul /= U.n_rowgroups;
-    const int split = (int)(ul % P.n_splits);
-    const int bq = (int)(ul / P.n_splits);
+    const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
+    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
