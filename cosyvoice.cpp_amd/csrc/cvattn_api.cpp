@@ -39,6 +39,7 @@ bool kv_ok(const cvattn_tensor *t) {
 struct FaShape {
     int n_q, H, H_kv, G, B, n_kv;
     int n_rows, n_rowgroups;
+    int n_khg; // kv-head groups (H_kv / kv heads per workgroup)
     FaKernelShape ks;
 };
 
@@ -71,11 +72,13 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     sh->B = (int)q->ne[3];
     sh->n_kv = (int)k->ne[1];
     sh->n_rows = sh->n_q * sh->G;
-    // 32-bit buffer offsets cover each K/V head view (decode kernel)
+    // 32-bit buffer offsets cover the K/V rows a decode workgroup reads (two heads when paired)
     const int64_t lim31 = ((int64_t)1 << 31) - 1;
-    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] < lim31 && (int64_t)v->ne[1] * (int64_t)v->nb[1] < lim31;
-    sh->ks = fa_shape(sh->n_rows, small);
+    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] + 2 * (int64_t)k->nb[2] < lim31 &&
+                       (int64_t)v->ne[1] * (int64_t)v->nb[1] + 2 * (int64_t)v->nb[2] < lim31;
+    sh->ks = fa_shape(sh->n_rows, sh->H_kv, small, mask && mask->data);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
+    sh->n_khg = sh->H_kv / sh->ks.hp;
     return CVATTN_OK;
 }
 
@@ -95,13 +98,15 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 // Token splits.  Decode-shaped problems (waves split the tokens) size each wave's token run so
 // the whole launch has ~kTargetWaves waves in flight; row-tiled problems split only when their
 // row groups alone cannot fill the chip.  `work` is the launch-wide sum of
-// B*H_kv*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
+// B*n_khg*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
 constexpr int64_t kTargetWaves = 2048;
+constexpr int64_t kSmallDecodeWork = 4 * 8192; // kv-head-group tokens of a latency-bound launch
 
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
     const int tstep = sh.ks.tstep;
     int len;
     if (sh.ks.wsplit) {
+        // tokens per wave: a multiple of the wave step (tstep tokens of hp kv heads)
         int64_t wlen = (std::max<int64_t>(1, work) + kTargetWaves - 1) / kTargetWaves;
         wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
         len = (int)wlen * sh.ks.nw;
@@ -113,16 +118,20 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         len = (n_kv + want - 1) / want;
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
     }
-    // never more splits than the in-kernel merge can weigh
     const int unit = sh.ks.wsplit ? tstep * sh.ks.nw : tstep;
-    const int min_len = (n_kv + sh.ks.max_splits - 1) / sh.ks.max_splits;
+    // Never more splits than the in-kernel merge takes in one pass.  The merging workgroup's
+    // loads are issued by one CU, so launches with enough work elsewhere (a few kv-head groups
+    // of long context or more) stop at half of that.
+    int max_splits = sh.ks.max_splits;
+    if (sh.ks.wsplit && work > kSmallDecodeWork) max_splits = std::max(1, max_splits / 2);
+    const int min_len = (n_kv + max_splits - 1) / max_splits;
     if (len < min_len) len = (min_len + unit - 1) / unit * unit;
     *split_len = len;
     *n_splits = n_kv > 0 ? (n_kv + len - 1) / len : 1;
 }
 
 int64_t split_work(const FaShape &sh) {
-    const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
+    const int64_t groups = (int64_t)sh.B * sh.n_khg * sh.n_rowgroups;
     return sh.ks.wsplit ? groups * sh.n_kv : groups;
 }
 
@@ -169,7 +178,8 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
     u.n_rowgroups = sh.n_rowgroups;
     u.q_f16 = q_type == T_F16 ? 1 : 0;
     u.scale_log2 = scale * 1.4426950408889634f;
-    u.div_hkv = make_fastdiv((uint32_t)sh.H_kv);
+    u.n_khg = sh.n_khg;
+    u.div_khg = make_fastdiv((uint32_t)sh.n_khg);
     u.div_rowgroups = make_fastdiv((uint32_t)sh.n_rowgroups);
     u.div_upp = make_fastdiv(1);
 }
@@ -178,7 +188,7 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
 constexpr int64_t kMaxUnits = ((int64_t)1 << 31) - 1;
 
 int64_t slots_per_split(const FaShape &sh) {
-    return (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * sh.ks.rows_per_group;
+    return (int64_t)sh.B * sh.n_khg * sh.n_rowgroups * sh.ks.rows_per_group;
 }
 
 // Plan for a single problem: splits and the workspace size.
@@ -249,7 +259,7 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
     a.p0.div_splits = make_fastdiv((uint32_t)pl.n_splits);
     a.p0.split_len = pl.split_len;
     a.u.n_problems = 1;
-    a.u.total_units = (int64_t)pl.sh.B * pl.sh.H_kv * pl.sh.n_rowgroups * pl.n_splits;
+    a.u.total_units = (int64_t)pl.sh.B * pl.sh.n_khg * pl.sh.n_rowgroups * pl.n_splits;
     if (a.u.total_units > kMaxUnits) return CVATTN_ERR_UNSUPPORTED;
     a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
     a.u.partials = (float *)ws;
@@ -283,6 +293,9 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         if (p.q.type != probs[0].q.type || p.k.type != probs[0].k.type || p.v.type != probs[0].v.type)
             return CVATTN_ERR_BAD_ARGS;
         if (sh.n_q != sh0->n_q || sh.H != sh0->H || sh.H_kv != sh0->H_kv || sh.B != sh0->B) return CVATTN_ERR_BAD_ARGS;
+        // one launch runs one kernel shape (e.g. a view too large for 32-bit offsets among
+        // decode problems cannot join them)
+        if (sh.ks.wsplit != sh0->ks.wsplit || sh.ks.hp != sh0->ks.hp) return CVATTN_ERR_UNSUPPORTED;
         work += split_work(sh);
     }
     if (table) table->resize(n);
@@ -302,7 +315,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         fp.part_begin = part;
         fp.row_begin = row;
         fp.cnt_begin = cnt;
-        const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
+        const int64_t groups = (int64_t)sh.B * sh.n_khg * sh.n_rowgroups;
         unit += groups * ns;
         if (ns > 1) {
             part += slots_per_split(sh) * ns;

@@ -95,7 +95,8 @@ struct FaUniform {
     int32_t q_f16;       // Q element type: 0 f32, 1 f16
     int32_t n_problems;
     float scale_log2;    // scale * log2(e)
-    FastDiv div_hkv, div_rowgroups, div_upp; // H_kv, n_rowgroups, units_per_problem
+    int32_t n_khg;       // kv-head groups per batch entry (H_kv / kv heads per workgroup)
+    FastDiv div_khg, div_rowgroups, div_upp; // n_khg, n_rowgroups, units_per_problem
     int64_t units_per_problem; // > 0 when every problem has this many workgroup units
     int64_t total_units;
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)

@@ -10,13 +10,14 @@ namespace cvattn {
 // Workgroup shape chosen for a problem: decode-shaped (<= 16 rows per kv head, waves split the
 // tokens) or row-tiled (waves split the rows).
 struct FaKernelShape {
-    bool wsplit;
+    bool wsplit;        // decode kernel (fa_decode.h)
+    int hp;             // kv heads per workgroup (decode kernel: 2 pairs heads of <= 8 rows)
     int nw;             // waves per workgroup
-    int tstep;          // tokens per staged tile (per wave when wsplit)
+    int tstep;          // tokens per staged tile (per wave step for the decode kernel)
     int rows_per_group; // query rows per workgroup
     int max_splits;     // most token splits one workgroup can merge in-kernel
 };
-FaKernelShape fa_shape(int n_rows, bool small_views);
+FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
 

@@ -2,21 +2,29 @@
 // (GQA decode over the LLM KV cache: the 7 q heads of a Qwen2-0.5B kv head times a few query
 // tokens), the GGML_OP_FLASH_ATTN_EXT node of src/cosyvoice-kv-cache.cpp:383-384 in decode.
 //
-// The KV cache is streamed once.  A workgroup is 4 waves sharing the 16 query rows of one
-// (batch, kv head); each wave owns a run of WLEN tokens and walks it in 64-token steps.  At the
-// first step every load of the step is issued before any use; later steps are prefetched one
-// step ahead.  K/V are read with bounds-checked buffer loads (rows past n_kv read as zeros).
+// The KV cache is streamed once, in whole ggml blocks.  A workgroup is 4 independent waves on
+// one (batch, kv-head group, token split); each wave walks its own run of tokens in steps of 32
+// token-heads and never waits for the other waves until the end.
 //
-// Per 16-token tile (v_mfma_f32_16x16x32_f16 with A = K rows, B = Q^T, see fa_impl.h for the
-// operand layouts): the K A-operand (8 consecutive dims of one token) is loaded straight into
-// registers and unpacked there; only the block scales go through LDS to reach the accumulator
-// layout.  V is staged transposed in wave-private LDS for the P.V MFMA.  Softmax is base 2 with
-// a lazily raised reference maximum (the O accumulators are rescaled only when a row's maximum
-// grows by more than 2^8, so P stays <= 256 and fits fp16).
+// Per wave step:
+//   * every lane loads one 32-dim block of K and one of V (16-byte buffer loads of whole blocks;
+//     64 lanes cover 16 consecutive tokens x 2 heads, or 32 tokens x 1 head, so a wave's loads
+//     are contiguous row runs), PD steps ahead of use;
+//   * the lane unpacks its blocks into a wave-private LDS tile of fp16 rows [token-head][64 dims]
+//     (K codes as "1024 + u", V codes exact) plus fp32 block scales;
+//   * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (A = K rows read from the tile, B = Q^T in
+//     registers, split into fp16 hi + lo parts for fp32-accurate scores);
+//   * softmax in base 2 with a lazily raised reference maximum;
+//   * O^T += V^T P^T with v_mfma_f32_16x16x16_f16: the S^T accumulator of a 16-token tile is
+//     already the B operand of P^T, and ds_read_b64_tr_b16 reads V^T straight from the
+//     token-major V tile.
+// With HP = 2 the two kv heads of a pair share one 16-row tile: rows 0-7 are the query rows of
+// head 2j, rows 8-15 those of head 2j+1 (up to 8 rows each), and each head's MFMA runs with the
+// other head's Q^T / P^T columns zero, so softmax work is spent on 14 live rows of 16.
 //
 // Token splits: the waves of a workgroup merge their states in LDS; several workgroups of one
-// (batch, kv head) write partials that the last one to arrive merges (prepared batches) or that
-// fa_combine_kernel merges (single calls).
+// group write partials that the last one to arrive merges (prepared batches) or that
+// dec_combine_kernel merges (single calls).
 #pragma once
 
 #include "fa_impl.h"
@@ -24,100 +32,202 @@
 namespace cvattn {
 
 constexpr int DEC_NW = 4;      // waves per workgroup
-constexpr int DEC_TS = 64;     // tokens per wave step
-constexpr int DEC_VSTR = 68;   // halfs per staged V^T row (64 tokens + pad)
+constexpr int DEC_RS = 72;     // halfs per canonical LDS row (64 dims + pad): 144 B
 constexpr float DEC_RESCALE_LOG2 = 8.0f;
-constexpr int DEC_MERGE_CHUNK = 16; // split partials loaded together by the merging workgroup
+constexpr int DEC_MERGE_CHUNK = 32; // most token splits per group (merged in one pass)
+
+typedef short short4_t __attribute__((ext_vector_type(4)));
 
 // Buffer resource over [base, base + bytes); loads past the end return 0.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(gu8 *base, int64_t bytes) {
     const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
     return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, n, 0x00020000);
 }
-
-__device__ __forceinline__ uint32_t bld_u32(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+__device__ __forceinline__ uint32_t bld_u16(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0);
 }
-__device__ __forceinline__ u2 bld_u64(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+__device__ __forceinline__ uint32_t bld_u32(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0);
 }
-__device__ __forceinline__ u4 bld_u128(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bld_u16(__amdgpu_buffer_rsrc_t r, int off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+__device__ __forceinline__ u4 bld_u128(__amdgpu_buffer_rsrc_t r, int v, int s) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
 }
 
-// raw8_load through a buffer resource: dims [32*b + 8*c, +8) of the head row at byte `row`.
+// ---- whole 32-dim blocks in registers ------------------------------------------------------
+
 template <int T>
-__device__ __forceinline__ void raw8_bload(__amdgpu_buffer_rsrc_t rs, int row, int b, int c, Raw8<T> &r) {
-    r.dm = 0u;
-    if constexpr (T == T_F32) {
-        const u4 a = bld_u128(rs, row + (32 * b + 8 * c) * 4);
-        const u4 e = bld_u128(rs, row + (32 * b + 8 * c) * 4 + 16);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            r.w[i] = a[i];
-            r.w[4 + i] = e[i];
-        }
-    } else if constexpr (T == T_F16) {
-        const u4 a = bld_u128(rs, row + (32 * b + 8 * c) * 2);
-#pragma unroll
-        for (int i = 0; i < 4; i++) r.w[i] = a[i];
-    } else {
-        const int blk = row + b * type_bytes(T);
-        r.dm = has_min(T) ? bld_u32(rs, blk) : bld_u16(rs, blk);
-        constexpr int qs_off = T == T_Q8_0 ? 2 : T == T_Q4_0 ? 2 : T == T_Q4_1 ? 4 : T == T_Q5_0 ? 6 : 8;
-        const u2 q = bld_u64(rs, blk + qs_off + (T == T_Q8_0 ? 8 * c : 8 * (c & 1)));
-        r.w[0] = q[0];
-        r.w[1] = q[1];
-        if constexpr (T == T_Q5_0 || T == T_Q5_1) r.w[2] = bld_u32(rs, blk + (T == T_Q5_0 ? 2 : 4));
-    }
+__host__ __device__ constexpr int blk_words() {
+    return T == T_F32 ? 32 : T == T_F16 ? 16 : T == T_Q8_0 ? 8 : 4;
 }
-
-template <int KT, int VT>
-struct DecRegs {
-    Raw8<KT> k[4][2]; // K A-operand words: tile x block (this lane's token, dims 8g..8g+7)
-    Raw8<VT> v[2][4]; // V staging items x 4 tokens
+// bytes of 32 consecutive dims of a head row
+template <int T>
+__host__ __device__ constexpr int dblk_bytes() {
+    return T == T_F32 ? 128 : T == T_F16 ? 64 : type_bytes(T);
+}
+template <int T>
+struct RawBlk {
+    uint32_t w[blk_words<T>()]; // codes (quantized) or values (f16/f32)
+    uint32_t dm;                // fp16 bits of d (low half) and m (high half)
+    uint32_t qh;                // 5th bits (q5_0/q5_1)
 };
 
-template <int KT>
-__device__ __forceinline__ void dec_load_k(__amdgpu_buffer_rsrc_t rk, int64_t nb1, int t0, int t16, int g,
-                                           Raw8<KT> (&k)[4][2]) {
+// Issue the loads of the 32-dim block at byte offset voff + soff of the resource.
+template <int T>
+__device__ __forceinline__ void blk_load(__amdgpu_buffer_rsrc_t rs, int voff, int soff, RawBlk<T> &r) {
+    r.dm = 0u;
+    r.qh = 0u;
+    constexpr int nq = T == T_F32 ? 8 : T == T_F16 ? 4 : T == T_Q8_0 ? 2 : 1;
+    constexpr int qoff = T == T_Q8_0 ? 2 : T == T_Q4_0 ? 2 : T == T_Q4_1 ? 4 : T == T_Q5_0 ? 6 : T == T_Q5_1 ? 8 : 0;
+    if constexpr (is_quant(T)) r.dm = has_min(T) ? bld_u32(rs, voff, soff) : bld_u16(rs, voff, soff);
+    if constexpr (T == T_Q5_0 || T == T_Q5_1) r.qh = bld_u32(rs, voff + (T == T_Q5_0 ? 2 : 4), soff);
 #pragma unroll
-    for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-        for (int b = 0; b < 2; b++) raw8_bload<KT>(rk, (int)((t0 + 16 * tt + t16) * nb1), b, g, k[tt][b]);
-}
-
-template <int VT>
-__device__ __forceinline__ void dec_load_v(__amdgpu_buffer_rsrc_t rv, int64_t nb1, int t0, int lane,
-                                           Raw8<VT> (&v)[2][4]) {
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const Item it = item_of(lane + 64 * i);
-#pragma unroll
-        for (int j = 0; j < 4; j++) raw8_bload<VT>(rv, (int)((t0 + 4 * it.tq + j) * nb1), it.b, it.c, v[i][j]);
+    for (int i = 0; i < nq; i++) {
+        const u4 a = bld_u128(rs, voff + qoff + 16 * i, soff);
+        r.w[4 * i + 0] = a[0];
+        r.w[4 * i + 1] = a[1];
+        r.w[4 * i + 2] = a[2];
+        r.w[4 * i + 3] = a[3];
     }
 }
 
-template <int KT, int VT, bool MASK, bool BATCH>
+// The Raw8 view (dims 8c..8c+7) of a whole block, for the shared unpackers.
+template <int T>
+__device__ __forceinline__ Raw8<T> blk_sub(const RawBlk<T> &r, int c) {
+    Raw8<T> s;
+    s.dm = r.dm;
+    if constexpr (T == T_F32) {
+#pragma unroll
+        for (int i = 0; i < 8; i++) s.w[i] = r.w[8 * c + i];
+    } else if constexpr (T == T_F16) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) s.w[i] = r.w[4 * c + i];
+    } else if constexpr (T == T_Q8_0) {
+        s.w[0] = r.w[2 * c];
+        s.w[1] = r.w[2 * c + 1];
+    } else {
+        s.w[0] = r.w[2 * (c & 1)];
+        s.w[1] = r.w[2 * (c & 1) + 1];
+        if constexpr (T == T_Q5_0 || T == T_Q5_1) s.w[2] = r.qh;
+    }
+    return s;
+}
+
+// Unpack a block into 32 fp16 of an LDS row (dims 32b..32b+31 at `dst`).  EXACT: V codes are
+// turned into the true small integers (u - code_off) with an exact fp16 subtraction; K keeps
+// "1024 + u" (its offset is folded into the score accumulator).
+template <int T, bool EXACT>
+__device__ __forceinline__ void blk_stage(const RawBlk<T> &r, _Float16 *dst) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        uint32_t o[4];
+        raw8_unpack<T>(blk_sub<T>(r, c), c, o);
+        if constexpr (EXACT && is_quant(T)) {
+            const _Float16 nb = (_Float16)(-(float)(1024 + code_off(T)));
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = __builtin_bit_cast(uint32_t, as_h2(o[i]) + h2{nb, nb});
+        }
+        *(u4 *)(dst + 8 * c) = u4{o[0], o[1], o[2], o[3]};
+    }
+}
+
+template <int T>
+__device__ __forceinline__ void blk_scales(const RawBlk<T> &r, float &d, float &m) {
+    Raw8<T> s;
+    s.dm = r.dm;
+    raw8_scales<T>(s, d, m);
+}
+
+// Steps whose raw blocks are in flight at once (register budget per type pair).
+template <int KT, int VT>
+__host__ __device__ constexpr int dec_prefetch() {
+    return blk_words<KT>() + blk_words<VT>() <= 16 ? 3 : blk_words<KT>() + blk_words<VT>() <= 32 ? 2 : 1;
+}
+
+// Query row of row slot `slot` (0..15) of a (kv-head group, row group); false if unused.
+template <int HP>
+__device__ __forceinline__ bool dec_row(const FaUniform &U, int khg, int rg, int slot, int &iq, int &hq) {
+    const int hs = HP == 2 ? slot >> 3 : 0;
+    const int rr = HP == 2 ? slot & 7 : rg * 16 + slot;
+    const int kh = khg * HP + hs;
+    const bool ok = rr < U.n_rows;
+    const int r = ok ? rr : 0;
+    iq = r / U.G;
+    hq = kh * U.G + r % U.G;
+    return ok;
+}
+
+// Split partials of one (batch, kv-head group, row group): O[16 row slots][ns][64] followed by
+// (m, l)[16 row slots][nsp][2] with nsp = ns rounded up to even (16-byte rows); this fits in the
+// 16 * ns * PART_STRIDE floats the host reserves per group.
+__device__ __forceinline__ int dec_ml_offset(int ns) { return 16 * ns * 64; }
+__device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
+
+// Merge the ns (<= DEC_MERGE_CHUNK) split partials of one group's 16 row slots into dst; thread =
+// (slot, 4 dims).  Every O load is issued before any is used; (m, l) pairs are loaded once per
+// row (two splits per lane) and their weights shared through the wave-private `sw` row.
+// SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
+template <int HP, bool SC1>
+__device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int khg,
+                                          int rg, int bq, float *sw) {
+    const int tid = threadIdx.x;
+    const int r = tid >> 4, q = tid & 15, d0 = 4 * q;
+    int iq, hq;
+    const bool ok = dec_row<HP>(U, khg, rg, r, iq, hq); // uniform over the row's 16 lanes
+    constexpr int AUX = SC1 ? 16 : 0;
+    const int nsp = dec_nsp(ns);
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc((gu8 *)part0, (int64_t)(dec_ml_offset(ns) + 16 * nsp * 2) * 4);
+    u4 ov[DEC_MERGE_CHUNK];
+#pragma unroll
+    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+        if (j < ns) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((r * ns + j) * 64 + d0) * 4, 0, AUX);
+    // lane q holds (m, l) of splits 2q and 2q+1
+    const u4 ml = __builtin_amdgcn_raw_buffer_load_b128(rp, (dec_ml_offset(ns) + (r * nsp + 2 * q) * 2) * 4, 0, AUX);
+    const bool v0 = 2 * q < ns, v1 = 2 * q + 1 < ns;
+    const float m0 = v0 ? as_f32(ml[0]) : -INFINITY, m1 = v1 ? as_f32(ml[2]) : -INFINITY;
+    float M = fmaxf(m0, m1);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    const float w0 = m0 == -INFINITY ? 0.0f : fast_exp2(m0 - Mu);
+    const float w1 = m1 == -INFINITY ? 0.0f : fast_exp2(m1 - Mu);
+    float L = (v0 ? as_f32(ml[1]) * w0 : 0.0f) + (v1 ? as_f32(ml[3]) * w1 : 0.0f);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) L += __shfl_xor(L, o);
+    float *row_w = sw + r * DEC_MERGE_CHUNK;
+    *(float2 *)&row_w[2 * q] = float2{w0, w1};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+        if (j < ns) acc += as_f4(ov[j]) * row_w[j];
+    if (!ok) return;
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
+}
+
+template <int KT, int VT, bool MASK, bool BATCH, int HP>
 __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
-    __shared__ __attribute__((aligned(16))) _Float16 sV[DEC_NW][HEAD * DEC_VSTR];
-    __shared__ __attribute__((aligned(16))) float sKd[DEC_NW][2][DEC_TS];
-    __shared__ __attribute__((aligned(16))) float sKm[DEC_NW][2][DEC_TS];
-    __shared__ __attribute__((aligned(16))) float sVd[DEC_NW][2][DEC_TS];
-    __shared__ __attribute__((aligned(16))) float sVm[DEC_NW][2][DEC_TS];
+    constexpr int TS = 32 / HP;                // tokens per wave step
+    constexpr int NT = HP == 2 ? 1 : 2;        // 16-token score tiles per step
+    constexpr int PD = dec_prefetch<KT, VT>(); // steps in flight
+    __shared__ __attribute__((aligned(16))) _Float16 sK[DEC_NW][32 * DEC_RS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[DEC_NW][32 * DEC_RS];
+    __shared__ __attribute__((aligned(16))) float sS[DEC_NW][4][2][32]; // {kd, km, vd, vm} x block x row
     __shared__ uint32_t s_last;
 
     const FaUniform &U = args.u;
     FaProblem P;
-    // consecutive units (the kv heads of one token range, whose rows share cache lines) run on
-    // one XCD so each line is fetched into one L2 only
+    // consecutive units (the kv-head groups of one token range, whose rows share cache lines)
+    // run on one XCD so each line is fetched into one L2 only
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
-    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
+    const int khg = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    // the wave index is uniform per wave: readfirstlane lets the token range, step loop and
+    // buffer soffsets live in scalar registers
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
 
     const int t_begin = split * P.split_len;
@@ -125,25 +235,39 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int wlen = P.split_len / DEC_NW;
     const int w_begin = t_begin + wv * wlen;
     const int w_end = min(t_end, w_begin + wlen);
-    const int nsteps = (min(wlen, max(0, t_end - t_begin)) + DEC_TS - 1) / DEC_TS; // uniform
+    const int nsteps = (max(0, w_end - w_begin) + TS - 1) / TS; // per wave
 
-    gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
-    gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
-    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, (int64_t)P.n_kv * P.k_nb1);
-    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, (int64_t)P.n_kv * P.v_nb1);
+    // this lane's block in every step: token lt of the step, row slot ls, 32-dim block lb
+    const int lt = HP == 2 ? lane >> 2 : lane >> 1;
+    const int ls = HP == 2 ? (lane >> 1) & 1 : lt >> 4;
+    const int lb = lane & 1;
+    const int lrow = 16 * ls + (lt & 15);
+    const int kh0 = khg * HP;
+    gu8 *kbase = gptr(P.k) + (int64_t)kh0 * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
+    gu8 *vbase = gptr(P.v) + (int64_t)kh0 * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
+    // the head rows this workgroup reads: loads of tokens >= n_kv fall outside and read 0
+    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + (int64_t)(HP - 1) * P.k_nb2 + 2 * dblk_bytes<KT>() : 0;
+    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + (int64_t)(HP - 1) * P.v_nb2 + 2 * dblk_bytes<VT>() : 0;
+    const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, kext);
+    const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, vext);
+    const int kvoff = lt * (int)P.k_nb1 + (HP == 2 ? ls * (int)P.k_nb2 : 0) + lb * dblk_bytes<KT>();
+    const int vvoff = lt * (int)P.v_nb1 + (HP == 2 ? ls * (int)P.v_nb2 : 0) + lb * dblk_bytes<VT>();
 
-    // issue the first step's K/V loads before anything else
-    DecRegs<KT, VT> R;
-    if (nsteps > 0) {
-        dec_load_k<KT>(rk, P.k_nb1, w_begin, col, g, R.k);
-        dec_load_v<VT>(rv, P.v_nb1, w_begin, lane, R.v);
+    // issue the first PD steps' loads before anything else
+    RawBlk<KT> RK[PD];
+    RawBlk<VT> RV[PD];
+#pragma unroll
+    for (int p = 0; p < PD; p++) {
+        if (p < nsteps) {
+            blk_load<KT>(rk, kvoff, (w_begin + p * TS) * (int)P.k_nb1, RK[p]);
+            blk_load<VT>(rv, vvoff, (w_begin + p * TS) * (int)P.v_nb1, RV[p]);
+        }
     }
 
-    // ---- this lane's query row and its Q operand (hi + lo fp16) ----
-    const int row = rg * 16 + col;
-    const bool row_ok = row < U.n_rows;
-    const int iq = row_ok ? row / U.G : 0;
-    const int hq = kh * U.G + (row_ok ? row % U.G : 0);
+    // ---- this lane's query row (MFMA column `col`) and its Q operand (hi + lo fp16) ----
+    int iq, hq;
+    const bool row_ok = dec_row<HP>(U, khg, rg, col, iq, hq);
+    const int hs = HP == 2 ? col >> 3 : 0; // head slot of this lane's row
     h8 qhi[2], qlo[2];
     float qsum[2];
     bool need_lo = false;
@@ -194,154 +318,157 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
     for (int i = 0; i < 4; i++) oacc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    _Float16 *cV = sV[wv];
-    for (int step = 0; step < nsteps; step++) {
-        const int t0 = w_begin + step * DEC_TS;
-        // ---- stage V^T and the block scales of K and V ----
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            Stage4<VT> s4;
-#pragma unroll
-            for (int j = 0; j < 4; j++) s4.r[j] = R.v[i][j];
-            s4.valid = 0xfu; // rows past n_kv were read as zeros; past w_end they are masked
-            stage_store_v<VT, DEC_VSTR, DEC_TS>(s4, item_of(lane + 64 * i), cV, sVd[wv], sVm[wv]);
-        }
-        if constexpr (is_quant(KT)) {
-            if (g < 2) {
-#pragma unroll
-                for (int tt = 0; tt < 4; tt++) {
-                    float d0, m0, d1, m1; // (select, not R.k[tt][g]: a lane-dependent index would
-                    raw8_scales<KT>(R.k[tt][0], d0, m0); // move the array to scratch memory)
-                    raw8_scales<KT>(R.k[tt][1], d1, m1);
-                    const float d = g == 0 ? d0 : d1, m = g == 0 ? m0 : m1;
-                    sKd[wv][g][16 * tt + col] = d;
-                    if constexpr (has_min(KT)) sKm[wv][g][16 * tt + col] = m;
-                }
-            }
-        }
-        __syncthreads();
-        if (step + 1 < nsteps) dec_load_v<VT>(rv, P.v_nb1, t0 + DEC_TS, lane, R.v);
+    _Float16 *tK = sK[wv], *tV = sV[wv];
+    float(*tS)[2][32] = sS[wv];
+    const h4 z4 = {};
 
-        // ---- S^T = K Q^T for the four 16-token tiles ----
-        f4 s[4];
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            uint32_t a0w[4], a1w[4];
-            raw8_unpack<KT>(R.k[tt][0], g, a0w);
-            raw8_unpack<KT>(R.k[tt][1], g, a1w);
-            const h8 a0 = as_h8(u4{a0w[0], a0w[1], a0w[2], a0w[3]});
-            const h8 a1 = as_h8(u4{a1w[0], a1w[1], a1w[2], a1w[3]});
-            f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
-            f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], cinit1, 0, 0, 0);
-            if (need_lo) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[0], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc1, 0, 0, 0);
-            }
-            if constexpr (is_quant(KT)) {
-                const f4 d0 = *(const f4 *)&sKd[wv][0][16 * tt + 4 * g];
-                const f4 d1 = *(const f4 *)&sKd[wv][1][16 * tt + 4 * g];
-                f4 v = d0 * acc0 + d1 * acc1;
-                if constexpr (has_min(KT)) {
-                    const f4 m0 = *(const f4 *)&sKm[wv][0][16 * tt + 4 * g];
-                    const f4 m1 = *(const f4 *)&sKm[wv][1][16 * tt + 4 * g];
-                    v += m0 * qsum[0] + m1 * qsum[1];
+        for (int p = 0; p < PD; p++) {
+            const int step = s0 + p;
+            if (step < nsteps) { // uniform
+                const int t0 = w_begin + step * TS;
+                // ---- unpack this step's blocks into the wave's tile, then refill the slot ----
+                blk_stage<KT, false>(RK[p], tK + lrow * DEC_RS + 32 * lb);
+                blk_stage<VT, true>(RV[p], tV + lrow * DEC_RS + 32 * lb);
+                {
+                    float d, m;
+                    blk_scales<KT>(RK[p], d, m);
+                    tS[0][lb][lrow] = d;
+                    if constexpr (has_min(KT)) tS[1][lb][lrow] = m;
+                    blk_scales<VT>(RV[p], d, m);
+                    tS[2][lb][lrow] = d;
+                    if constexpr (has_min(VT)) tS[3][lb][lrow] = m;
                 }
-                s[tt] = v;
-            } else {
-                s[tt] = acc0 + acc1;
-            }
-        }
-        if (step + 1 < nsteps) dec_load_k<KT>(rk, P.k_nb1, t0 + DEC_TS, col, g, R.k);
+                if (step + PD < nsteps) {
+                    blk_load<KT>(rk, kvoff, (t0 + PD * TS) * (int)P.k_nb1, RK[p]);
+                    blk_load<VT>(rv, vvoff, (t0 + PD * TS) * (int)P.v_nb1, RV[p]);
+                }
+                // the tile is wave-private: LDS keeps one wave's accesses in order
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-        // ---- mask, range, softmax with a lazily raised reference maximum ----
-        const bool full = t0 + DEC_TS <= w_end; // uniform
-        float mx = -INFINITY;
+                // ---- scores: NT tiles of 16 tokens x 16 rows (S^T, lane = row col, tokens 4g+j) ----
+                f4 sc[NT];
 #pragma unroll
-        for (int tt = 0; tt < 4; tt++) {
-            const int tb = t0 + 16 * tt + 4 * g;
-            if constexpr (MASK) {
-                if (full) {
-                    const u2 mw = ldg_u64(mrow + (int64_t)tb * 2);
-                    const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
-                    s[tt][0] += (float)a[0] * 1.4426950408889634f;
-                    s[tt][1] += (float)a[1] * 1.4426950408889634f;
-                    s[tt][2] += (float)c2[0] * 1.4426950408889634f;
-                    s[tt][3] += (float)c2[1] * 1.4426950408889634f;
-                } else {
+                for (int s = 0; s < NT; s++) {
+                    // HP = 2: both heads' K rows against all 16 query rows; each lane keeps the
+                    // accumulator of its own row's head
+                    f4 acc[2];
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int t = tb + j;
-                        const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
-                        s[tt][j] = t < w_end ? s[tt][j] + mv * 1.4426950408889634f : -INFINITY;
+                    for (int b = 0; b < 2; b++) {
+                        const f4 ci = b ? cinit1 : cinit0;
+                        const h8 a0 = *(const h8 *)(tK + (16 * (HP == 2 ? 0 : s) + col) * DEC_RS + 32 * b + 8 * g);
+                        f4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[b], ci, 0, 0, 0);
+                        if (need_lo) c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[b], c0, 0, 0, 0);
+                        if constexpr (HP == 2) {
+                            const h8 a1 = *(const h8 *)(tK + (16 + col) * DEC_RS + 32 * b + 8 * g);
+                            f4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[b], ci, 0, 0, 0);
+                            if (need_lo) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[b], c1, 0, 0, 0);
+                            // (element-wise selects: a select of whole vectors became a stack array)
+#pragma unroll
+                            for (int j = 0; j < 4; j++) c0[j] = hs ? c1[j] : c0[j];
+                        }
+                        acc[b] = c0;
+                    }
+                    const int sb = 16 * (HP == 2 ? hs : s) + 4 * g; // scale rows of these tokens
+                    if constexpr (is_quant(KT)) {
+                        const f4 d0 = *(const f4 *)&tS[0][0][sb];
+                        const f4 d1 = *(const f4 *)&tS[0][1][sb];
+                        f4 v = d0 * acc[0] + d1 * acc[1];
+                        if constexpr (has_min(KT)) {
+                            const f4 m0 = *(const f4 *)&tS[1][0][sb];
+                            const f4 m1 = *(const f4 *)&tS[1][1][sb];
+                            v += m0 * qsum[0] + m1 * qsum[1];
+                        }
+                        sc[s] = v;
+                    } else {
+                        sc[s] = acc[0] + acc[1];
                     }
                 }
-            } else if (!full) {
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (tb + j >= w_end) s[tt][j] = -INFINITY;
-            }
-#pragma unroll
-            for (int j = 0; j < 4; j++) mx = fmaxf(mx, s[tt][j]);
-        }
-        mx = wave_max16x4(mx);
-        // raise the reference only when the row maximum outgrows it by 2^8
-        const bool raise = mx > m_ref + DEC_RESCALE_LOG2;
-        const float m_new = raise ? mx : m_ref;
-        if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
-            const float alpha = fast_exp2(m_ref - m_new);
-            l_run *= alpha;
-            corr[0] *= alpha;
-            corr[1] *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; i++) oacc[i] *= alpha;
-        }
-        m_ref = m_new;
-        const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
-#pragma unroll
-        for (int tt = 0; tt < 4; tt++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = fast_exp2(s[tt][j] - m_use);
-                s[tt][j] = p;
-                l_run += p;
-            }
 
-        // ---- O^T += V^T P^T ----
+                // ---- mask, range, softmax with a lazily raised reference maximum ----
+                const bool full = t0 + TS <= w_end; // uniform
+                float mx = -INFINITY;
 #pragma unroll
-        for (int kb = 0; kb < 2; kb++) {
-            const f4 plo = s[2 * kb], phi = s[2 * kb + 1];
-            h8 pb[2];
+                for (int s = 0; s < NT; s++) {
+                    const int tb = t0 + 16 * s + 4 * g;
+                    if constexpr (MASK) {
+                        if (full) {
+                            const u2 mw = ldg_u64(mrow + (int64_t)tb * 2);
+                            const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
+                            sc[s][0] += (float)a[0] * 1.4426950408889634f;
+                            sc[s][1] += (float)a[1] * 1.4426950408889634f;
+                            sc[s][2] += (float)c2[0] * 1.4426950408889634f;
+                            sc[s][3] += (float)c2[1] * 1.4426950408889634f;
+                        } else {
 #pragma unroll
-            for (int b = 0; b < 2; b++) {
-                f4 xlo = plo, xhi = phi;
-                if constexpr (is_quant(VT)) {
-                    xlo = plo * *(const f4 *)&sVd[wv][b][32 * kb + 4 * g];
-                    xhi = phi * *(const f4 *)&sVd[wv][b][32 * kb + 16 + 4 * g];
+                            for (int j = 0; j < 4; j++) {
+                                const int t = tb + j;
+                                const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
+                                sc[s][j] = t < w_end ? sc[s][j] + mv * 1.4426950408889634f : -INFINITY;
+                            }
+                        }
+                    } else if (!full) {
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            if (tb + j >= w_end) sc[s][j] = -INFINITY;
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) mx = fmaxf(mx, sc[s][j]);
                 }
+                mx = wave_max16x4(mx);
+                const bool raise = mx > m_ref + DEC_RESCALE_LOG2;
+                const float m_new = raise ? mx : m_ref;
+                if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
+                    const float alpha = fast_exp2(m_ref - m_new);
+                    l_run *= alpha;
+                    corr[0] *= alpha;
+                    corr[1] *= alpha;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    pb[b][j] = (_Float16)xlo[j];
-                    pb[b][4 + j] = (_Float16)xhi[j];
+                    for (int i = 0; i < 4; i++) oacc[i] *= alpha;
                 }
-                if constexpr (has_min(VT)) {
-                    const f4 mlo = *(const f4 *)&sVm[wv][b][32 * kb + 4 * g];
-                    const f4 mhi = *(const f4 *)&sVm[wv][b][32 * kb + 16 + 4 * g];
-                    const f4 t = plo * mlo + phi * mhi;
-                    corr[b] += t[0] + t[1] + t[2] + t[3];
-                }
-                if constexpr (!is_quant(VT)) break;
-            }
-            if constexpr (!is_quant(VT)) pb[1] = pb[0];
+                m_ref = m_new;
+                const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
+
+                // ---- P^T operands (V block scale folded in) and O^T += V^T P^T ----
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int dim = 16 * i + col;
-                const h4 va = *(const h4 *)&cV[dim * DEC_VSTR + 32 * kb + 4 * g];
-                const h4 vb = *(const h4 *)&cV[dim * DEC_VSTR + 32 * kb + 16 + 4 * g];
-                const h8 a = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-                oacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[i >> 1], oacc[i], 0, 0, 0);
+                for (int s = 0; s < NT; s++) {
+                    f4 p;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        p[j] = fast_exp2(sc[s][j] - m_use);
+                        l_run += p[j];
+                    }
+                    const int sb = 16 * (HP == 2 ? hs : s) + 4 * g;
+                    h4 pb[2];
+#pragma unroll
+                    for (int b = 0; b < 2; b++) {
+                        f4 x = p;
+                        if constexpr (is_quant(VT)) x = p * *(const f4 *)&tS[2][b][sb];
+                        pb[b] = h4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+                        if constexpr (has_min(VT)) {
+                            const f4 t = p * *(const f4 *)&tS[3][b][sb];
+                            corr[b] += t[0] + t[1] + t[2] + t[3];
+                        }
+                    }
+#pragma unroll
+                    for (int h = 0; h < HP; h++) {
+                        // V^T operand rows: tokens 4g..4g+3 of this tile, dims 16i + col
+                        const int vrow = 16 * (HP == 2 ? h : s) + 4 * g + (col >> 2);
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (__attribute__((address_space(3))) short4_t *)(tV + vrow * DEC_RS + 16 * i + 4 * (col & 3)));
+                            const h4 a = __builtin_bit_cast(h4, raw);
+                            const h4 bop = (HP == 1 || hs == h) ? pb[i >> 1] : z4;
+                            oacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, oacc[i], 0, 0, 0);
+                        }
+                    }
+                }
             }
         }
-        __syncthreads();
     }
 
     // ---------------- epilogue: merge the 4 waves (same rows, disjoint tokens) ----------------
@@ -352,9 +479,10 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
         for (int i = 0; i < 4; i++) oacc[i] += corr[i >> 1];
     }
-    float *xo = (float *)&sV[0][0];                  // [4][64 dims][16 rows]
-    float *xm = (float *)&sKd[0][0][0];              // [4][16] m, then [4][16] l
-    static_assert(sizeof(sV) >= DEC_NW * 64 * 16 * sizeof(float), "merge buffer");
+    __syncthreads(); // every wave is done with its tile: reuse them for the merge
+    float *xo = (float *)&sK[0][0]; // [4][64 dims][16 rows]
+    float *xm = &sS[0][0][0][0];    // [4][16] m, then [4][16] l
+    static_assert(sizeof(sK) >= DEC_NW * 64 * 16 * sizeof(float), "merge buffer");
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
@@ -377,9 +505,10 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
         for (int j = 0; j < 4; j++) o[j] += xo[(w * 64 + 16 * wv + 4 * g + j) * 16 + col] * f;
     }
-    // wave wv now owns dims 16*wv + 4g + j of row `col`
+    // wave wv now owns dims 16*wv + 4g + j of row slot `col`
     const int ns = P.n_splits;
-    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * 16 * ns;
+    const int64_t grp = ((int64_t)bq * U.n_khg + khg) * U.n_rowgroups + rg;
+    const int64_t slot0 = P.part_begin + grp * 16 * ns;
     if (ns == 1) {
         if (row_ok) {
             const float inv = L > 0.0f ? 1.0f / L : 0.0f;
@@ -388,35 +517,30 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         return;
     }
+    float *part0 = U.partials + slot0 * PART_STRIDE;
+    const int o_off = ((col * ns + split) * 64 + 16 * wv + 4 * g) * 4;
+    const int ml_off = (dec_ml_offset(ns) + (col * dec_nsp(ns) + split) * 2) * 4;
     if constexpr (!BATCH) {
-        float *part = U.partials + (slot0 + (int64_t)col * ns + split) * PART_STRIDE;
         if (row_ok) {
-            *(f4 *)&part[16 * wv + 4 * g] = o;
-            if (wv == 0 && g == 0) {
-                part[64] = M;
-                part[65] = L;
-            }
+            *(f4 *)((char *)part0 + o_off) = o;
+            if (wv == 0 && g == 0) *(float2 *)((char *)part0 + ml_off) = float2{M, L};
         }
         return;
     } else {
-        // Partials of this (batch, kv head, row group): [16 rows][ns splits][PART_STRIDE floats],
-        // written and read with agent-coherent (sc1) buffer accesses, the form the compiler gives
-        // agent-scope atomic loads and stores, but vectorised and all in flight at once.
+        // Partials are written and read with agent-coherent (sc1) buffer accesses, the form the
+        // compiler gives agent-scope atomic loads and stores, but vectorised and all in flight.
         constexpr int SC1 = 16;
-        const __amdgpu_buffer_rsrc_t rp =
-            make_rsrc((gu8 *)(U.partials + slot0 * PART_STRIDE), (int64_t)16 * ns * PART_STRIDE * 4);
+        const __amdgpu_buffer_rsrc_t rp = make_rsrc((gu8 *)part0, (int64_t)16 * ns * PART_STRIDE * 4);
         if (row_ok) {
-            const int base = (col * ns + split) * PART_STRIDE * 4;
-            __builtin_amdgcn_raw_buffer_store_b128(as_u4(o), rp, base + (16 * wv + 4 * g) * 4, 0, SC1);
-            if (wv == 0 && g == 0)
-                __builtin_amdgcn_raw_buffer_store_b64(u2{as_u32(M), as_u32(L)}, rp, base + 64 * 4, 0, SC1);
+            __builtin_amdgcn_raw_buffer_store_b128(as_u4(o), rp, o_off, 0, SC1);
+            if (wv == 0 && g == 0) __builtin_amdgcn_raw_buffer_store_b64(u2{as_u32(M), as_u32(L)}, rp, ml_off, 0, SC1);
         }
         // once the partials have completed, the arrival count publishes them (a device-wide
         // fence would write back the whole L2)
         wait_memory();
         __syncthreads();
         if (tid == 0) {
-            uint32_t *cnt = U.counters + P.cnt_begin + ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
+            uint32_t *cnt = U.counters + P.cnt_begin + grp;
             const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const bool last = prev == (uint32_t)(ns - 1);
             if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -424,45 +548,22 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         __syncthreads();
         if (!s_last) return;
-        // last arrival: merge every split of its 16 rows; thread = (row, 4 dims); the loads of
-        // up to DEC_MERGE_CHUNK splits are issued together
-        const int r = tid >> 4, d0 = (tid & 15) * 4;
-        const int rrow = rg * 16 + r;
-        if (rrow >= U.n_rows) return;
-        float Mm = -INFINITY, Ll = 0.0f;
-        f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int c0 = 0; c0 < ns; c0 += DEC_MERGE_CHUNK) {
-            u2 ml[DEC_MERGE_CHUNK];
-            u4 ov[DEC_MERGE_CHUNK];
-#pragma unroll
-            for (int j = 0; j < DEC_MERGE_CHUNK; j++) {
-                const int sp = min(c0 + j, ns - 1);
-                const int base = (r * ns + sp) * PART_STRIDE * 4;
-                ml[j] = __builtin_amdgcn_raw_buffer_load_b64(rp, base + 64 * 4, 0, SC1);
-                ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, base + d0 * 4, 0, SC1);
-            }
-            float cm = Mm;
-#pragma unroll
-            for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-                if (c0 + j < ns) cm = fmaxf(cm, as_f32(ml[j][0]));
-            if (cm == -INFINITY) continue; // every row of these splits is fully masked so far
-            const float a = fast_exp2(Mm - cm);
-            Ll *= a;
-            acc *= a;
-#pragma unroll
-            for (int j = 0; j < DEC_MERGE_CHUNK; j++) {
-                if (c0 + j < ns) {
-                    const float f = fast_exp2(as_f32(ml[j][0]) - cm);
-                    Ll += as_f32(ml[j][1]) * f;
-                    acc += as_f4(ov[j]) * f;
-                }
-            }
-            Mm = cm;
-        }
-        const float inv = Ll > 0.0f ? 1.0f / Ll : 0.0f;
-        const int riq = rrow / U.G, rhq = kh * U.G + rrow % U.G;
-        *(f4 *)&P.dst[(((int64_t)bq * U.n_q + riq) * U.H + rhq) * HEAD + d0] = acc * inv;
+        dec_merge<HP, true>(U, P, part0, ns, khg, rg, bq, &sS[0][0][0][0]);
     }
+}
+
+// Single calls: merge the split partials the decode kernel wrote; one workgroup per group.
+template <int HP>
+__global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
+    __shared__ __attribute__((aligned(16))) float sw[16 * DEC_MERGE_CHUNK];
+    const FaUniform &U = args.u;
+    const FaProblem &P = args.p0;
+    const int64_t grp = blockIdx.x;
+    const int rg = (int)(grp % U.n_rowgroups);
+    const int khg = (int)((grp / U.n_rowgroups) % U.n_khg);
+    const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.n_khg));
+    dec_merge<HP, false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, khg,
+                         rg, bq, sw);
 }
 
 } // namespace cvattn

@@ -1,9 +1,12 @@
 // fa_dispatch.hip -- picks the flash-attention instantiation for a launch.
-#include "fa_impl.h"
+#include "fa_decode_inst.h"
 
 namespace cvattn {
 
-FaLaunchFn fa_pick_decode(int mask, int batch, int ki, int vi);
+static FaLaunchFn fa_pick_decode(int mask, int batch, int hp, int ki, int vi) {
+    if (mask) return fa_pick_decode_m1_h1(batch, ki, vi);
+    return hp == 2 ? fa_pick_decode_m0_h2(batch, ki, vi) : fa_pick_decode_m0_h1(batch, ki, vi);
+}
 FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
 
 static int type_index(int t) {
@@ -19,15 +22,17 @@ static int type_index(int t) {
     }
 }
 
-FaKernelShape fa_shape(int n_rows, bool small_views) {
+FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask) {
     FaKernelShape s;
-    // decode-shaped kernel (fa_decode.h): <= 16 rows, and K/V views addressable with 32-bit
-    // buffer offsets; everything else runs the row-tiled kernel
+    // decode-shaped kernel (fa_decode.h): <= 16 rows per kv head and K/V views addressable with
+    // 32-bit buffer offsets; kv heads are paired when each has <= 8 rows (the masked variant
+    // keeps one head per workgroup); everything else runs the row-tiled kernel
     s.wsplit = n_rows <= 16 && small_views;
+    s.hp = s.wsplit && n_rows <= 8 && h_kv % 2 == 0 && !mask ? 2 : 1;
     s.nw = 4;
-    s.tstep = s.wsplit ? 64 : FaCfg<4, false>::TSTEP;
+    s.tstep = s.wsplit ? 32 / s.hp : FaCfg<4, false>::TSTEP;
     s.rows_per_group = s.wsplit ? 16 : FaCfg<4, false>::ROWS;
-    s.max_splits = s.wsplit ? (1 << 20) : FaCfg<4, false>::MERGE_MAX_SPLITS;
+    s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : FaCfg<4, false>::MERGE_MAX_SPLITS;
     return s;
 }
 
@@ -35,7 +40,7 @@ hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bo
                      hipStream_t st) {
     const int ki = type_index(ktype), vi = type_index(vtype);
     if (ki < 0 || vi < 0) return hipErrorInvalidValue;
-    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
+    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, s.hp, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
     return fn(a, st);
 }
 

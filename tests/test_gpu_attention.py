@@ -140,6 +140,19 @@ def test_decode_ragged_lengths(eng, orc, rng, nkv, cuda):
     run_case(eng, orc, c, what=f"nkv {nkv}")
 
 
+@pytest.mark.parametrize("H,Hkv,nq,B,kB", [(6, 3, 1, 1, 1),     # odd kv heads: one head per workgroup
+                                            (8, 4, 1, 2, 1),     # two head pairs, K/V broadcast over batch
+                                            (16, 2, 1, 1, 1),    # 8 rows per head: full head slots
+                                            (4, 2, 3, 1, 1),     # 6 rows per head over 3 query tokens
+                                            (18, 2, 1, 1, 1)])   # 9 rows per head: no pairing
+def test_decode_head_grouping(eng, orc, rng, H, Hkv, nq, B, kB, cuda):
+    """Kv-head pairing of the decode kernel (two heads of <= 8 rows share a 16-row tile) and the
+    fallbacks around it, with splits over several workgroups (n_kv 2500)."""
+    for kt, vt in ((Q8_0, Q4_0), (F16, Q5_1)):
+        c = llm_case(orc, rng, H=H, Hkv=Hkv, nq=nq, nkv=2500, kt=kt, vt=vt, B=B, kB=kB, max_seq=2600)
+        run_case(eng, orc, c, what=f"H {H} Hkv {Hkv} nq {nq} B {B} k{kt} v{vt}")
+
+
 def test_decode_two_query_tokens(eng, orc, rng, cuda):
     c = llm_case(orc, rng, nq=2, nkv=700, kt=Q8_0, vt=Q4_0, max_seq=1024)
     run_case(eng, orc, c, what="nq 2")
