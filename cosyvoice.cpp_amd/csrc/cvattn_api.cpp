@@ -177,6 +177,7 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
     u.n_rows = sh.n_rows;
     u.n_rowgroups = sh.n_rowgroups;
     u.q_f16 = q_type == T_F16 ? 1 : 0;
+    u.scale = scale;
     u.scale_log2 = scale * 1.4426950408889634f;
     u.n_khg = sh.n_khg;
     u.div_khg = make_fastdiv((uint32_t)sh.n_khg);

@@ -94,6 +94,7 @@ struct FaUniform {
     int32_t n_rowgroups; // ceil(n_rows / rows per workgroup)
     int32_t q_f16;       // Q element type: 0 f32, 1 f16
     int32_t n_problems;
+    float scale;         // softmax scale
     float scale_log2;    // scale * log2(e)
     int32_t n_khg;       // kv-head groups per batch entry (H_kv / kv heads per workgroup)
     FastDiv div_khg, div_rowgroups, div_upp; // n_khg, n_rowgroups, units_per_problem

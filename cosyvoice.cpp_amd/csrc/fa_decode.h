@@ -36,107 +36,6 @@ constexpr int DEC_RS = 72;     // halfs per canonical LDS row (64 dims + pad): 1
 constexpr float DEC_RESCALE_LOG2 = 8.0f;
 constexpr int DEC_MERGE_CHUNK = 32; // most token splits per group (merged in one pass)
 
-typedef short short4_t __attribute__((ext_vector_type(4)));
-
-// Buffer resource over [base, base + bytes); loads past the end return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(gu8 *base, int64_t bytes) {
-    const int32_t n = bytes > 0x7fffffff ? 0x7fffffff : (int32_t)bytes;
-    return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ uint32_t bld_u16(__amdgpu_buffer_rsrc_t r, int v, int s) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, v, s, 0);
-}
-__device__ __forceinline__ uint32_t bld_u32(__amdgpu_buffer_rsrc_t r, int v, int s) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, v, s, 0);
-}
-__device__ __forceinline__ u4 bld_u128(__amdgpu_buffer_rsrc_t r, int v, int s) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, v, s, 0);
-}
-
-// ---- whole 32-dim blocks in registers ------------------------------------------------------
-
-template <int T>
-__host__ __device__ constexpr int blk_words() {
-    return T == T_F32 ? 32 : T == T_F16 ? 16 : T == T_Q8_0 ? 8 : 4;
-}
-// bytes of 32 consecutive dims of a head row
-template <int T>
-__host__ __device__ constexpr int dblk_bytes() {
-    return T == T_F32 ? 128 : T == T_F16 ? 64 : type_bytes(T);
-}
-template <int T>
-struct RawBlk {
-    uint32_t w[blk_words<T>()]; // codes (quantized) or values (f16/f32)
-    uint32_t dm;                // fp16 bits of d (low half) and m (high half)
-    uint32_t qh;                // 5th bits (q5_0/q5_1)
-};
-
-// Issue the loads of the 32-dim block at byte offset voff + soff of the resource.
-template <int T>
-__device__ __forceinline__ void blk_load(__amdgpu_buffer_rsrc_t rs, int voff, int soff, RawBlk<T> &r) {
-    r.dm = 0u;
-    r.qh = 0u;
-    constexpr int nq = T == T_F32 ? 8 : T == T_F16 ? 4 : T == T_Q8_0 ? 2 : 1;
-    constexpr int qoff = T == T_Q8_0 ? 2 : T == T_Q4_0 ? 2 : T == T_Q4_1 ? 4 : T == T_Q5_0 ? 6 : T == T_Q5_1 ? 8 : 0;
-    if constexpr (is_quant(T)) r.dm = has_min(T) ? bld_u32(rs, voff, soff) : bld_u16(rs, voff, soff);
-    if constexpr (T == T_Q5_0 || T == T_Q5_1) r.qh = bld_u32(rs, voff + (T == T_Q5_0 ? 2 : 4), soff);
-#pragma unroll
-    for (int i = 0; i < nq; i++) {
-        const u4 a = bld_u128(rs, voff + qoff + 16 * i, soff);
-        r.w[4 * i + 0] = a[0];
-        r.w[4 * i + 1] = a[1];
-        r.w[4 * i + 2] = a[2];
-        r.w[4 * i + 3] = a[3];
-    }
-}
-
-// The Raw8 view (dims 8c..8c+7) of a whole block, for the shared unpackers.
-template <int T>
-__device__ __forceinline__ Raw8<T> blk_sub(const RawBlk<T> &r, int c) {
-    Raw8<T> s;
-    s.dm = r.dm;
-    if constexpr (T == T_F32) {
-#pragma unroll
-        for (int i = 0; i < 8; i++) s.w[i] = r.w[8 * c + i];
-    } else if constexpr (T == T_F16) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) s.w[i] = r.w[4 * c + i];
-    } else if constexpr (T == T_Q8_0) {
-        s.w[0] = r.w[2 * c];
-        s.w[1] = r.w[2 * c + 1];
-    } else {
-        s.w[0] = r.w[2 * (c & 1)];
-        s.w[1] = r.w[2 * (c & 1) + 1];
-        if constexpr (T == T_Q5_0 || T == T_Q5_1) s.w[2] = r.qh;
-    }
-    return s;
-}
-
-// Unpack a block into 32 fp16 of an LDS row (dims 32b..32b+31 at `dst`).  EXACT: V codes are
-// turned into the true small integers (u - code_off) with an exact fp16 subtraction; K keeps
-// "1024 + u" (its offset is folded into the score accumulator).
-template <int T, bool EXACT>
-__device__ __forceinline__ void blk_stage(const RawBlk<T> &r, _Float16 *dst) {
-#pragma unroll
-    for (int c = 0; c < 4; c++) {
-        uint32_t o[4];
-        raw8_unpack<T>(blk_sub<T>(r, c), c, o);
-        if constexpr (EXACT && is_quant(T)) {
-            const _Float16 nb = (_Float16)(-(float)(1024 + code_off(T)));
-#pragma unroll
-            for (int i = 0; i < 4; i++) o[i] = __builtin_bit_cast(uint32_t, as_h2(o[i]) + h2{nb, nb});
-        }
-        *(u4 *)(dst + 8 * c) = u4{o[0], o[1], o[2], o[3]};
-    }
-}
-
-template <int T>
-__device__ __forceinline__ void blk_scales(const RawBlk<T> &r, float &d, float &m) {
-    Raw8<T> s;
-    s.dm = r.dm;
-    raw8_scales<T>(s, d, m);
-}
-
 // Steps whose raw blocks are in flight at once (register budget per type pair).
 template <int KT, int VT>
 __host__ __device__ constexpr int dec_prefetch() {
@@ -254,8 +153,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int vvoff = lt * (int)P.v_nb1 + (HP == 2 ? ls * (int)P.v_nb2 : 0) + lb * dblk_bytes<VT>();
 
     // issue the first PD steps' loads before anything else
-    RawBlk<KT> RK[PD];
-    RawBlk<VT> RV[PD];
+    RawBuf<blk_words<KT>()> RK[PD];
+    RawBuf<blk_words<VT>()> RV[PD];
 #pragma unroll
     for (int p = 0; p < PD; p++) {
         if (p < nsteps) {

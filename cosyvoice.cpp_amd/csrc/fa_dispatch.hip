@@ -30,9 +30,9 @@ FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask) {
     s.wsplit = n_rows <= 16 && small_views;
     s.hp = s.wsplit && n_rows <= 8 && h_kv % 2 == 0 && !mask ? 2 : 1;
     s.nw = 4;
-    s.tstep = s.wsplit ? 32 / s.hp : FaCfg<4, false>::TSTEP;
-    s.rows_per_group = s.wsplit ? 16 : FaCfg<4, false>::ROWS;
-    s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : FaCfg<4, false>::MERGE_MAX_SPLITS;
+    s.tstep = s.wsplit ? 32 / s.hp : ROWS_TS;
+    s.rows_per_group = s.wsplit ? 16 : ROWS_ROWS;
+    s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : ROWS_MERGE_MAX_SPLITS;
     return s;
 }
 

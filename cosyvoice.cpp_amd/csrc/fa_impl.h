@@ -1,54 +1,45 @@
 // fa_impl.h -- flash attention for gfx950 (the GGML_OP_FLASH_ATTN_EXT node of
-// src/cosyvoice-kv-cache.cpp:383-384 and src/cosyvoice-graph.cpp:375-376).
+// src/cosyvoice-kv-cache.cpp:383-384 and src/cosyvoice-graph.cpp:375-376): the row-tiled kernel
+// for prefill, DiT and every problem with more than 16 query rows per kv head, plus what all
+// attention kernels share (problem lookup, workgroup decomposition, split merges).
 //
 // Rows.  For one (batch b, kv head kh) the rows are the n_q * G query rows sharing kh
 // (G = H / H_kv), ordered r = i * G + g (query i, q head kh*G + g).  A wave owns 16 rows: the 16
-// columns of its MFMA tiles.  For GQA decode the 7 q heads of a kv head are rows of one wave, so
-// every K/V byte is read once for all of them.
-//
-// Two workgroup shapes (template WSPLIT):
-//   WSPLIT (decode, <= 16 rows):  NW waves share one row group and split the workgroup's token
-//       range; each wave stages its own 32-token tiles; the waves' softmax states are merged in
-//       LDS at the end, so a workgroup writes one result (or one split partial).
-//   rows   (prefill / DiT):       NW waves own 16 rows each (64 rows per workgroup) and share
-//       64-token K/V tiles staged once in LDS.
-// Token splits beyond one workgroup are merged by fa_combine_kernel.
+// columns of its MFMA tiles.  A workgroup is 4 waves (64 rows) sharing 64-token K/V tiles that
+// are staged once per step into LDS, double-buffered: while the waves compute tile s, the
+// tile s+1 is unpacked into the other buffer from registers loaded two steps ahead, so a step
+// has one barrier.
 //
 // Per wave and 16-token tile (v_mfma_f32_16x16x32_f16, two 32-dim K halves):
-//   S^T[t][r] = K[t][:] . Q[r][:]     A = K rows from LDS (natural layout), B = Q^T (registers)
-// Q is pre-scaled by scale*log2(e), so softmax runs in base 2.  Quantized K is staged as fp16
-// "1024 + u" codes; the MFMA accumulator starts at -(1024 + off)*sum(Q) so it ends as
-// sum(code*Q), and the block scale d (and min m) are applied per token afterwards.
-// The C layout of S^T (lane l: row l%16, tokens 4*(l/16)+j) is exactly the B layout of P^T for
-//   O^T[dim][r] += V^T[dim][t] . P^T[t][r]   A = V^T from LDS (staged transposed), B = P^T
+//   S^T[t][r] = K[t][:] . Q[r][:]     A = K rows from the LDS tile, B = Q^T (registers)
+// Quantized K is staged as fp16 "1024 + u" codes; the accumulator starts at -(1024 + off)*sum(Q)
+// so it ends as sum(code*Q), and the block scale d (and min m) are applied per token afterwards.
+// Q*scale is kept exactly in fp16 when it can be (f16 Q with a power-of-two scale: the scores
+// are then turned into base 2 with one multiply); otherwise Q*scale*log2(e) is split into fp16
+// hi + lo parts and two MFMAs give fp32-accurate scores.
+// The C layout of S^T (lane l: row l%16, tokens 4*(l/16)+j) is the B layout of P^T for
+//   O^T[dim][r] += V^T[dim][t] . P^T[t][r]
 // when the 8 k-slots of lane group g are tokens {4g..4g+3} of one 16-token tile and
-// {16+4g..16+4g+3} of the next.  V codes are staged exactly (fp16 small integers); the V block
+// {16+4g..16+4g+3} of the next; the A operand V^T comes from the token-major V tile through two
+// ds_read_b64_tr_b16 per MFMA.  V codes are staged exactly (fp16 small integers); the V block
 // scale is folded into P (one B operand per 32-dim block) and the V min into a per-row term.
-//
-// Pipelining: the global loads of step s+1 are issued into registers before step s computes.
+// Softmax is base 2 with a lazily raised reference maximum (rescale only when a row maximum grows
+// by more than 2^8).
 #pragma once
 
 #include "cvattn_device.h"
 #include "cvattn_launch.h"
+#include "kv_blocks.h"
 
 namespace cvattn {
 
-template <int NW, bool WSPLIT>
-struct FaCfg {
-    static constexpr int TSTEP = WSPLIT ? 32 : 64;  // tokens per staged tile
-    static constexpr int NTILE = TSTEP / 16;         // 16-token S tiles per step
-    static constexpr int NKB = TSTEP / 32;           // 32-token PV k-blocks per step
-    static constexpr int KSTR = 72;                  // halfs per staged K row (64 + pad)
-    static constexpr int VSTR = TSTEP + 4;           // halfs per staged V^T row (+ pad)
-    static constexpr int NITEM = TSTEP * 2;          // staging items per tensor per tile
-    static constexpr int NSTAGE = WSPLIT ? NW : 1;   // independent tile buffers
-    static constexpr int ROWS = WSPLIT ? 16 : 16 * NW; // query rows per workgroup
-    static constexpr int THREADS = 64 * NW;
-    // staging items handled per thread per step (K and V counted together)
-    static constexpr int ITEMS_PER_THREAD = WSPLIT ? 2 : (2 * NITEM) / THREADS;
-    // the K tile buffers double as the split-merge scratch
-    static constexpr int MERGE_MAX_SPLITS = (NSTAGE * TSTEP * KSTR * 2 / 4) / (2 * ROWS);
-};
+constexpr int ROWS_NW = 4;          // waves (16 rows each) per workgroup
+constexpr int ROWS_TS = 64;         // tokens per staged tile
+constexpr int ROWS_RS = 72;         // halfs per LDS tile row (64 dims + pad)
+constexpr int ROWS_ROWS = 16 * ROWS_NW;
+constexpr float ROWS_RESCALE_LOG2 = 8.0f;
+// the two K tile buffers double as the split-merge scratch (2 * ROWS * n_splits floats)
+constexpr int ROWS_MERGE_MAX_SPLITS = (2 * ROWS_TS * ROWS_RS * 2 / 4) / (2 * ROWS_ROWS);
 
 // Index of the problem owning `key` in a table sorted by `field`: start at the proportional
 // guess (exact when all problems have the same size) and walk; uniform across the workgroup.
@@ -106,98 +97,6 @@ __device__ __forceinline__ UnitPos locate_unit(const FaArgs &args, uint32_t unit
     return r;
 }
 
-// Staging item: 4 consecutive tokens x 8 consecutive dims of one 32-dim block.
-struct Item {
-    int c, b, tq;
-};
-__device__ __forceinline__ Item item_of(int it) { return Item{it & 3, (it >> 2) & 1, it >> 3}; }
-
-template <int T>
-struct Stage4 {
-    Raw8<T> r[4];
-    uint32_t valid; // bit j: token j of the item is inside the wave's range
-};
-
-// Issue the loads of one staging item.  Rows past `t_lim` read row min(t, n_kv-1) (always in
-// bounds) and are zeroed when stored; nothing here touches the loaded registers, so the loads
-// stay in flight while the current tile computes.
-template <int T>
-__device__ __forceinline__ void stage_load(gu8 *base, int64_t nb1, int t0, int t_lim, int n_kv, Item it,
-                                           Stage4<T> &s) {
-    s.valid = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int t = t0 + 4 * it.tq + j;
-        raw8_load<T>(base + (int64_t)min(t, n_kv - 1) * nb1, it.b, it.c, s.r[j]);
-        s.valid |= (t < t_lim ? 1u : 0u) << j;
-    }
-}
-
-template <int T>
-__device__ __forceinline__ void stage_unpack(const Stage4<T> &s, int j, int c, uint32_t o[4], float &d, float &m) {
-    const bool ok = (s.valid >> j) & 1u;
-    raw8_unpack<T>(s.r[j], c, o);
-    if (!ok) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) o[i] = is_quant(T) ? 0x64006400u : 0u; // code 0 / value 0
-    }
-    raw8_scales<T>(s.r[j], d, m);
-    d = ok ? d : 0.0f;
-    m = ok ? m : 0.0f;
-}
-
-// K tile: natural layout sK[t][dim], scales sKd/sKm[b][t].
-template <int T, int KSTR, int TSTEP>
-__device__ __forceinline__ void stage_store_k(const Stage4<T> &s, Item it, _Float16 *sK, float (*sKd)[TSTEP],
-                                              float (*sKm)[TSTEP]) {
-    float d[4], m[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        uint32_t o[4];
-        stage_unpack<T>(s, j, it.c, o, d[j], m[j]);
-        *(u4 *)&sK[(4 * it.tq + j) * KSTR + 32 * it.b + 8 * it.c] = u4{o[0], o[1], o[2], o[3]};
-    }
-    if constexpr (is_quant(T)) {
-        if (it.c == 0) {
-            *(f4 *)&sKd[it.b][4 * it.tq] = f4{d[0], d[1], d[2], d[3]};
-            if constexpr (has_min(T)) *(f4 *)&sKm[it.b][4 * it.tq] = f4{m[0], m[1], m[2], m[3]};
-        }
-    }
-}
-
-// V tile: transposed sV[dim][t] holding the exact code (or value) as fp16, scales sVd/sVm[b][t].
-template <int T, int VSTR, int TSTEP>
-__device__ __forceinline__ void stage_store_v(const Stage4<T> &s, Item it, _Float16 *sV, float (*sVd)[TSTEP],
-                                              float (*sVm)[TSTEP]) {
-    constexpr float bias = stage_bias<T>();
-    const h2 nb2 = {(_Float16)(-bias), (_Float16)(-bias)};
-    h2 hv[4][4];
-    float d[4], m[4];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        uint32_t o[4];
-        stage_unpack<T>(s, j, it.c, o, d[j], m[j]);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            h2 x = as_h2(o[i]);
-            if constexpr (is_quant(T)) x = x + nb2;
-            hv[j][i] = x;
-        }
-    }
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int i = e >> 1, k = e & 1;
-        const h4 col4 = {hv[0][i][k], hv[1][i][k], hv[2][i][k], hv[3][i][k]};
-        *(h4 *)&sV[(32 * it.b + 8 * it.c + e) * VSTR + 4 * it.tq] = col4;
-    }
-    if constexpr (is_quant(T)) {
-        if (it.c == 0) {
-            *(f4 *)&sVd[it.b][4 * it.tq] = f4{d[0], d[1], d[2], d[3]};
-            if constexpr (has_min(T)) *(f4 *)&sVm[it.b][4 * it.tq] = f4{m[0], m[1], m[2], m[3]};
-        }
-    }
-}
-
 // Last-arriving workgroup of a split row group merges all split partials of its rows
 // (prepared batches: no separate combine launch).  Three phases so the global loads run in
 // parallel: (1) every split's (m, l) of every row into LDS, (2) one thread per row turns them
@@ -246,56 +145,62 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
     }
 }
 
-template <int NW, bool WSPLIT, int KT, int VT, bool MASK, bool BATCH>
-__global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
-    using C = FaCfg<NW, WSPLIT>;
-    constexpr int TSTEP = C::TSTEP, NTILE = C::NTILE, NKB = C::NKB;
-    constexpr int KSTR = C::KSTR, VSTR = C::VSTR, NITEM = C::NITEM, NSTAGE = C::NSTAGE;
-
-    __shared__ __attribute__((aligned(16))) _Float16 sK[NSTAGE][TSTEP * KSTR];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[NSTAGE][HEAD * VSTR];
-    __shared__ __attribute__((aligned(16))) float sKd[NSTAGE][2][TSTEP];
-    __shared__ __attribute__((aligned(16))) float sKm[NSTAGE][2][TSTEP];
-    __shared__ __attribute__((aligned(16))) float sVd[NSTAGE][2][TSTEP];
-    __shared__ __attribute__((aligned(16))) float sVm[NSTAGE][2][TSTEP];
+template <int KT, int VT, bool MASK, bool BATCH>
+__global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
+    constexpr int TS = ROWS_TS, RS = ROWS_RS, NTILE = TS / 16, NKB = TS / 32;
+    constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][TS * RS];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TS * RS];
+    __shared__ __attribute__((aligned(16))) float sS[2][4][2][TS]; // {kd, km, vd, vm} x block x token
 
     const FaUniform &U = args.u;
     FaProblem P;
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
     const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wv = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15; // MFMA column (query row) / A-operand row (token or dim)
     const int g = lane >> 4;   // lane group: k-slots 8g..8g+7, C rows 4g..4g+3
-    const int st = WSPLIT ? wv : 0;
 
-    // token range of this workgroup, and of this wave's tiles
     const int t_begin = split * P.split_len;
     const int t_end = min(P.n_kv, t_begin + P.split_len);
-    const int wlen = WSPLIT ? P.split_len / NW : P.split_len;
-    const int w_begin = WSPLIT ? t_begin + wv * wlen : t_begin;
-    const int w_end = WSPLIT ? min(t_end, w_begin + wlen) : t_end;
-    const int nsteps = (min(wlen, max(0, t_end - t_begin)) + TSTEP - 1) / TSTEP; // uniform in the workgroup
+    const int nsteps = (max(0, t_end - t_begin) + TS - 1) / TS; // uniform
 
+    // ---- staging role: waves 0-1 stage K blocks, waves 2-3 V blocks; thread = (token, block) ----
+    const bool stage_k = wv < 2; // uniform per wave
+    const int st_tok = (tid & 127) >> 1, st_b = tid & 1;
     gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
     gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
+    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
+    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>() : 0;
+    const __amdgpu_buffer_rsrc_t rsrc = stage_k ? make_rsrc(kbase, kext) : make_rsrc(vbase, vext);
+    const int nb1 = stage_k ? (int)P.k_nb1 : (int)P.v_nb1;
+    const int voff = st_tok * nb1 + st_b * (stage_k ? dblk_bytes<KT>() : dblk_bytes<VT>());
+
+    RawBuf<W> R0, R1;
+    auto load_tile = [&](int t0, RawBuf<W> &r) {
+        if (stage_k)
+            blk_load<KT>(rsrc, voff, t0 * nb1, r);
+        else
+            blk_load<VT>(rsrc, voff, t0 * nb1, r);
+    };
 
     // ---- this lane's query row and its Q operand (B of the S^T MFMA) ----
-    const int row = rg * C::ROWS + (WSPLIT ? 0 : wv * 16) + col;
+    const int row = rg * ROWS_ROWS + wv * 16 + col;
     const bool row_ok = row < U.n_rows;
     const int iq = row_ok ? row / U.G : 0;
     const int hq = kh * U.G + (row_ok ? row % U.G : 0);
-    // Q*scale*log2(e) = hi + lo, both fp16: two MFMAs make the QK products fp32-accurate
-    // (lo is zero when Q is f16 and the scale is a power of two, and its MFMA is skipped then).
+
+    if (nsteps > 0) load_tile(t_begin, R0);
+    if (nsteps > 1) load_tile(t_begin + TS, R1);
+
     h8 qhi[2], qlo[2];
     float qsum[2];
-    bool need_lo = false;
+    float smul; // multiplies the staged K scales / raw scores into base-2 logits
+    bool need_lo;
     {
         gu8 *qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)bq * P.q_nb3;
-        // independent scalar loads, all issued before any use (16-byte vector loads of Q were
-        // miscompiled here by the ROCm 7.2 compiler: only two lanes of each load survived)
         float x[2][8];
         if (U.q_f16) { // uniform
 #pragma unroll
@@ -306,74 +211,88 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
 #pragma unroll
             for (int b = 0; b < 2; b++)
 #pragma unroll
-                for (int j = 0; j < 8; j++)
-                    x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
+                for (int j = 0; j < 8; j++) x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
         }
+        // Q*scale exact in fp16 for every row of the workgroup?
+        bool inexact = false;
+#pragma unroll
+        for (int b = 0; b < 2; b++)
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const float xs = row_ok ? x[b][j] * U.scale : 0.0f;
+                inexact |= (float)(_Float16)xs != xs;
+            }
+        need_lo = __syncthreads_or(inexact) != 0;
+        const float qmul = need_lo ? U.scale_log2 : U.scale;
+        smul = need_lo ? 1.0f : 1.4426950408889634f;
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float xs = row_ok ? x[b][j] * U.scale_log2 : 0.0f;
+                const float xs = row_ok ? x[b][j] * qmul : 0.0f;
                 const _Float16 hx = (_Float16)xs;
                 const _Float16 lx = (_Float16)(xs - (float)hx);
                 qhi[b][j] = hx;
                 qlo[b][j] = lx;
-                need_lo |= lx != (_Float16)0.0f;
                 s += (float)hx + (float)lx;
             }
             qsum[b] = wave_sum16x4(s);
         }
     }
-    need_lo = __syncthreads_or(need_lo) != 0;
     constexpr float kbias = stage_bias<KT>();
     const f4 cinit0 = {-kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0]};
     const f4 cinit1 = {-kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1]};
 
+    // unpack a staged tile's blocks into LDS buffer `buf`
+    auto write_tile = [&](const RawBuf<W> &r, int buf) {
+        float d, m;
+        if (stage_k) {
+            blk_stage<KT, false>(r, sK[buf] + st_tok * RS + 32 * st_b);
+            blk_scales<KT>(r, d, m);
+            sS[buf][0][st_b][st_tok] = d * smul;
+            if constexpr (has_min(KT)) sS[buf][1][st_b][st_tok] = m * smul;
+        } else {
+            blk_stage<VT, true>(r, sV[buf] + st_tok * RS + 32 * st_b);
+            blk_scales<VT>(r, d, m);
+            sS[buf][2][st_b][st_tok] = d;
+            if constexpr (has_min(VT)) sS[buf][3][st_b][st_tok] = m;
+        }
+    };
+
     gu8 *mrow = nullptr;
-    if constexpr (MASK) {
+    if constexpr (MASK)
         mrow = gptr(P.mask) + (int64_t)iq * P.m_nb1 + (int64_t)(hq % P.m_ne2) * P.m_nb2 +
                (int64_t)(bq % P.m_ne3) * P.m_nb3;
-    }
 
-    float m_run = -INFINITY;
+    float m_ref = -INFINITY; // reference maximum (base 2) of this lane's row
     float l_run = 0.0f;
     float corr[2] = {0.0f, 0.0f};
     f4 oacc[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) oacc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
-    // ---- staging assignment ----
-    // WSPLIT: every lane of a wave stages K item `lane` and V item `lane` of its own tile.
-    // rows:   thread t < NITEM stages K item t, else V item t - NITEM (uniform per wave).
-    const bool do_k = WSPLIT || tid < NITEM;
-    const bool do_v = WSPLIT || tid >= NITEM;
-    const Item itk = item_of(WSPLIT ? lane : tid);
-    const Item itv = item_of(WSPLIT ? lane : tid - NITEM);
-    Stage4<KT> rk;
-    Stage4<VT> rv;
-    if (nsteps > 0) {
-        if (do_k) stage_load<KT>(kbase, P.k_nb1, w_begin, w_end, P.n_kv, itk, rk);
-        if (do_v) stage_load<VT>(vbase, P.v_nb1, w_begin, w_end, P.n_kv, itv, rv);
-    }
-
-    for (int step = 0; step < nsteps; step++) {
-        const int t0 = w_begin + step * TSTEP;
-        if (do_k) stage_store_k<KT, KSTR, TSTEP>(rk, itk, sK[st], sKd[st], sKm[st]);
-        if (do_v) stage_store_v<VT, VSTR, TSTEP>(rv, itv, sV[st], sVd[st], sVm[st]);
-        __syncthreads();
-        if (step + 1 < nsteps) { // next tile's loads fly while this one computes
-            if (do_k) stage_load<KT>(kbase, P.k_nb1, t0 + TSTEP, w_end, P.n_kv, itk, rk);
-            if (do_v) stage_load<VT>(vbase, P.v_nb1, t0 + TSTEP, w_end, P.n_kv, itv, rv);
-        }
-
-        // ---------------- S^T = K Q^T, tile by tile ----------------
-        const _Float16 *cK = sK[st];
+    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS)
+    auto compute_tile = [&](int buf, int t0) {
+        const _Float16 *cK = sK[buf];
+        const _Float16 *cV = sV[buf];
+        float(*cS)[2][TS] = sS[buf];
         f4 s[NTILE];
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
-            const h8 a0 = *(const h8 *)&cK[(16 * tt + col) * KSTR + 8 * g];
-            const h8 a1 = *(const h8 *)&cK[(16 * tt + col) * KSTR + 32 + 8 * g];
+            const h8 a0 = *(const h8 *)&cK[(16 * tt + col) * RS + 8 * g];
+            const h8 a1 = *(const h8 *)&cK[(16 * tt + col) * RS + 32 + 8 * g];
+            if constexpr (!is_quant(KT)) {
+                // no block scales: one accumulator chain over both halves (its init is 0)
+                f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], acc, 0, 0, 0);
+                if (need_lo) {
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[0], acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc, 0, 0, 0);
+                }
+                s[tt] = acc;
+                continue;
+            }
             f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
             f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], cinit1, 0, 0, 0);
             if (need_lo) {
@@ -381,23 +300,24 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc1, 0, 0, 0);
             }
             if constexpr (is_quant(KT)) {
-                const f4 d0 = *(const f4 *)&sKd[st][0][16 * tt + 4 * g];
-                const f4 d1 = *(const f4 *)&sKd[st][1][16 * tt + 4 * g];
+                const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
+                const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
                 f4 v = d0 * acc0 + d1 * acc1;
                 if constexpr (has_min(KT)) {
-                    const f4 m0 = *(const f4 *)&sKm[st][0][16 * tt + 4 * g];
-                    const f4 m1 = *(const f4 *)&sKm[st][1][16 * tt + 4 * g];
+                    const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
+                    const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
                     v += m0 * qsum[0] + m1 * qsum[1];
                 }
                 s[tt] = v;
-            } else {
-                s[tt] = acc0 + acc1;
             }
         }
+        // scores so far are base-2 logits divided by sm2 (quantized K has smul folded into its
+        // scales); the mask path turns them into base-2 logits here, the others in the exponent
+        float sm2 = is_quant(KT) ? 1.0f : smul;
 
-        // ---------------- mask, bounds, online softmax (base 2) ----------------
+        // ---- mask, bounds, softmax with a lazily raised reference maximum ----
         float mx = -INFINITY;
-        const bool full = t0 + TSTEP <= w_end; // uniform: the whole tile is in range
+        const bool full = t0 + TS <= t_end; // uniform
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
             const int tb = t0 + 16 * tt + 4 * g;
@@ -405,50 +325,50 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                 if (full) {
                     const u2 mw = ldg_u64(mrow + (int64_t)tb * 2);
                     const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
-                    s[tt][0] += (float)a[0] * 1.4426950408889634f;
-                    s[tt][1] += (float)a[1] * 1.4426950408889634f;
-                    s[tt][2] += (float)c2[0] * 1.4426950408889634f;
-                    s[tt][3] += (float)c2[1] * 1.4426950408889634f;
+                    s[tt][0] = s[tt][0] * sm2 + (float)a[0] * 1.4426950408889634f;
+                    s[tt][1] = s[tt][1] * sm2 + (float)a[1] * 1.4426950408889634f;
+                    s[tt][2] = s[tt][2] * sm2 + (float)c2[0] * 1.4426950408889634f;
+                    s[tt][3] = s[tt][3] * sm2 + (float)c2[1] * 1.4426950408889634f;
                 } else {
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
                         const int t = tb + j;
                         const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
-                        s[tt][j] = t < w_end ? s[tt][j] + mv * 1.4426950408889634f : -INFINITY;
+                        s[tt][j] = t < t_end ? s[tt][j] * sm2 + mv * 1.4426950408889634f : -INFINITY;
                     }
                 }
-            } else {
-                if (!full) {
+            } else if (!full) {
 #pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        if (tb + j >= w_end) s[tt][j] = -INFINITY;
-                }
+                for (int j = 0; j < 4; j++)
+                    if (tb + j >= t_end) s[tt][j] = -INFINITY;
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) mx = fmaxf(mx, s[tt][j]);
         }
-        mx = wave_max16x4(mx);
-        const float m_new = fmaxf(m_run, mx);
-        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-        const float alpha = fast_exp2(m_run - m_use);
-        m_run = m_new;
-        float psum = 0.0f;
+        if constexpr (MASK) sm2 = 1.0f;
+        mx = wave_max16x4(mx) * sm2;
+        const bool raise = mx > m_ref + ROWS_RESCALE_LOG2;
+        const float m_new = raise ? mx : m_ref;
+        if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
+            const float alpha = fast_exp2(m_ref - m_new);
+            l_run *= alpha;
+            corr[0] *= alpha;
+            corr[1] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; i++) oacc[i] *= alpha;
+        }
+        m_ref = m_new;
+        const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float p = fast_exp2(s[tt][j] - m_use);
+                const float p = fast_exp2(__builtin_fmaf(s[tt][j], sm2, -m_use));
                 s[tt][j] = p;
-                psum += p;
+                l_run += p;
             }
-        l_run = l_run * alpha + psum;
-        corr[0] *= alpha;
-        corr[1] *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; i++) oacc[i] *= alpha;
 
-        // ---------------- O^T += V^T P^T ----------------
-        const _Float16 *cV = sV[st];
+        // ---- O^T += V^T P^T (32 tokens per MFMA: tiles 2kb and 2kb+1) ----
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const f4 plo = s[2 * kb], phi = s[2 * kb + 1];
@@ -457,8 +377,8 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
             for (int b = 0; b < 2; b++) {
                 f4 xlo = plo, xhi = phi;
                 if constexpr (is_quant(VT)) {
-                    xlo = plo * *(const f4 *)&sVd[st][b][32 * kb + 4 * g];
-                    xhi = phi * *(const f4 *)&sVd[st][b][32 * kb + 16 + 4 * g];
+                    xlo = plo * *(const f4 *)&cS[2][b][32 * kb + 4 * g];
+                    xhi = phi * *(const f4 *)&cS[2][b][32 * kb + 16 + 4 * g];
                 }
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -466,29 +386,57 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                     pb[b][4 + j] = (_Float16)xhi[j];
                 }
                 if constexpr (has_min(VT)) {
-                    const f4 mlo = *(const f4 *)&sVm[st][b][32 * kb + 4 * g];
-                    const f4 mhi = *(const f4 *)&sVm[st][b][32 * kb + 16 + 4 * g];
+                    const f4 mlo = *(const f4 *)&cS[3][b][32 * kb + 4 * g];
+                    const f4 mhi = *(const f4 *)&cS[3][b][32 * kb + 16 + 4 * g];
                     const f4 t = plo * mlo + phi * mhi;
                     corr[b] += t[0] + t[1] + t[2] + t[3];
                 }
                 if constexpr (!is_quant(VT)) break; // one B operand serves both blocks
             }
             if constexpr (!is_quant(VT)) pb[1] = pb[0];
+            const int vrow = 32 * kb + 4 * g + (col >> 2);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const int dim = 16 * i + col;
-                const h4 va = *(const h4 *)&cV[dim * VSTR + 32 * kb + 4 * g];
-                const h4 vb = *(const h4 *)&cV[dim * VSTR + 32 * kb + 16 + 4 * g];
-                const h8 a = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+                const _Float16 *va = cV + vrow * RS + 16 * i + 4 * (col & 3);
+                const h4 lo = __builtin_bit_cast(
+                    h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)va));
+                const h4 hi = __builtin_bit_cast(
+                    h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) short4_t *)(va + 16 * RS)));
+                const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 oacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[i >> 1], oacc[i], 0, 0, 0);
             }
+        }
+    };
+
+    // ---- pipeline: tile s computes from LDS while tile s+1 is unpacked into the other buffer
+    //      from registers loaded two steps earlier ----
+    if (nsteps > 0) {
+        write_tile(R0, 0);
+        if (nsteps > 2) load_tile(t_begin + 2 * TS, R0);
+    }
+    __syncthreads();
+    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+        // even step: compute buffer 0, stage tile s0+1 (R1) into buffer 1
+        compute_tile(0, t_begin + s0 * TS);
+        if (s0 + 1 < nsteps) {
+            write_tile(R1, 1);
+            if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TS, R1);
+        }
+        __syncthreads();
+        if (s0 + 1 >= nsteps) break;
+        // odd step: compute buffer 1, stage tile s0+2 (R0) into buffer 0
+        compute_tile(1, t_begin + (s0 + 1) * TS);
+        if (s0 + 2 < nsteps) {
+            write_tile(R0, 0);
+            if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TS, R0);
         }
         __syncthreads();
     }
 
     // ---------------- epilogue ----------------
     // partial slot of (row r of this row group, split s) = slot0 + r * n_splits + s
-    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * C::ROWS * P.n_splits;
+    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * ROWS_ROWS * P.n_splits;
     l_run = wave_sum16x4(l_run);
     if constexpr (has_min(VT)) {
         corr[0] = wave_sum16x4(corr[0]);
@@ -496,83 +444,29 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
 #pragma unroll
         for (int i = 0; i < 4; i++) oacc[i] += corr[i >> 1];
     }
-
-    if constexpr (WSPLIT && NW > 1) {
-        // merge the NW waves' states (same rows, disjoint tokens) through LDS
-        float *xo = (float *)&sK[0][0];                    // [NW][64 dims][16 rows]
-        float *xm = (float *)&sV[0][0];                    // [NW][16] m then [NW][16] l
-        static_assert(sizeof(sK) >= NW * 64 * 16 * sizeof(float), "merge buffer");
+    if (row_ok) {
+        if (P.n_splits == 1) {
+            const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
+            float *o = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i] * inv;
+        } else {
+            float *o = U.partials + (slot0 + (int64_t)(row - rg * ROWS_ROWS) * P.n_splits + split) * PART_STRIDE;
+            if constexpr (BATCH) {
 #pragma unroll
-            for (int j = 0; j < 4; j++) xo[(wv * 64 + 16 * i + 4 * g + j) * 16 + col] = oacc[i][j];
-        if (g == 0) {
-            xm[wv * 16 + col] = m_run;
-            xm[NW * 16 + wv * 16 + col] = l_run;
-        }
-        __syncthreads();
-        float M = -INFINITY;
+                for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int w = 0; w < NW; w++) M = fmaxf(M, xm[w * 16 + col]);
-        const float Mu = M == -INFINITY ? 0.0f : M;
-        float L = 0.0f;
-        f4 o = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int w = 0; w < NW; w++) {
-            const float f = fast_exp2(xm[w * 16 + col] - Mu);
-            L += xm[NW * 16 + w * 16 + col] * f;
-#pragma unroll
-            for (int j = 0; j < 4; j++) o[j] += xo[(w * 64 + 16 * wv + 4 * g + j) * 16 + col] * f;
-        }
-        // wave wv now owns dims 16*wv + 4g + j of row `col`
-        if (row_ok) {
-            if (P.n_splits == 1) {
-                const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-                float *out = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
-                *(f4 *)&out[16 * wv + 4 * g] = o * inv;
-            } else {
-                float *out = U.partials + (slot0 + (int64_t)col * P.n_splits + split) * PART_STRIDE;
-                if constexpr (BATCH) {
-#pragma unroll
-                    for (int j = 0; j < 4; j++) st_agent(&out[16 * wv + 4 * g + j], o[j]);
-                    if (wv == 0 && g == 0) {
-                        st_agent(&out[64], M);
-                        st_agent(&out[65], L);
-                    }
-                } else {
-                    *(f4 *)&out[16 * wv + 4 * g] = o;
-                    if (wv == 0 && g == 0) {
-                        out[64] = M;
-                        out[65] = L;
-                    }
+                    for (int j = 0; j < 4; j++) st_agent(&o[16 * i + 4 * g + j], oacc[i][j]);
+                if (g == 0) {
+                    st_agent(&o[64], m_ref);
+                    st_agent(&o[65], l_run);
                 }
-            }
-        }
-    } else {
-        if (row_ok) {
-            if (P.n_splits == 1) {
-                const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-                float *o = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
-#pragma unroll
-                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i] * inv;
             } else {
-                float *o = U.partials + (slot0 + (int64_t)(row - rg * C::ROWS) * P.n_splits + split) * PART_STRIDE;
-                if constexpr (BATCH) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++)
-#pragma unroll
-                        for (int j = 0; j < 4; j++) st_agent(&o[16 * i + 4 * g + j], oacc[i][j]);
-                    if (g == 0) {
-                        st_agent(&o[64], m_run);
-                        st_agent(&o[65], l_run);
-                    }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i];
-                    if (g == 0) {
-                        o[64] = m_run;
-                        o[65] = l_run;
-                    }
+                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i];
+                if (g == 0) {
+                    o[64] = m_ref;
+                    o[65] = l_run;
                 }
             }
         }
@@ -595,7 +489,7 @@ __global__ __launch_bounds__(64 * NW) void fa_fwd_kernel(FaArgs args) {
                 s_last = last ? 1u : 0u;
             }
             __syncthreads();
-            if (s_last) merge_splits<C::ROWS, C::THREADS>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
+            if (s_last) merge_splits<ROWS_ROWS, 64 * ROWS_NW>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
         }
     }
 }
@@ -641,32 +535,31 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
 
 using FaLaunchFn = hipError_t (*)(const FaArgs &, hipStream_t);
 
-template <int NW, bool WSPLIT, int KT, int VT, bool MASK, bool BATCH>
-hipError_t launch_fa(const FaArgs &a, hipStream_t st) {
+template <int KT, int VT, bool MASK, bool BATCH>
+hipError_t launch_rows(const FaArgs &a, hipStream_t st) {
     if (a.u.total_units <= 0) return hipSuccess;
-    hipLaunchKernelGGL((fa_fwd_kernel<NW, WSPLIT, KT, VT, MASK, BATCH>), dim3((unsigned)a.u.total_units),
-                       dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH>), dim3((unsigned)a.u.total_units), dim3(64 * ROWS_NW), 0,
+                       st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // single calls merge split partials with a second launch; prepared batches merge in-kernel
     if (!BATCH && a.p0.n_splits > 1 && a.u.total_rows > 0) {
-        hipLaunchKernelGGL((fa_combine_kernel<FaCfg<NW, WSPLIT>::ROWS, BATCH>), dim3((unsigned)a.u.total_rows),
-                           dim3(64), 0, st, a);
+        hipLaunchKernelGGL((fa_combine_kernel<ROWS_ROWS, BATCH>), dim3((unsigned)a.u.total_rows), dim3(64), 0, st, a);
         e = hipGetLastError();
     }
     return e;
 }
 
-// Launch table [mask][batch][k type index][v type index]; index order f32 f16 q8_0 q4_0 q4_1 q5_0 q5_1.
-#define CVATTN_V_ROW(NW, WS, KT, MASK, BATCH)                                                       \
-    {launch_fa<NW, WS, KT, T_F32, MASK, BATCH>, launch_fa<NW, WS, KT, T_F16, MASK, BATCH>,          \
-     launch_fa<NW, WS, KT, T_Q8_0, MASK, BATCH>, launch_fa<NW, WS, KT, T_Q4_0, MASK, BATCH>,        \
-     launch_fa<NW, WS, KT, T_Q4_1, MASK, BATCH>, launch_fa<NW, WS, KT, T_Q5_0, MASK, BATCH>,        \
-     launch_fa<NW, WS, KT, T_Q5_1, MASK, BATCH>}
-#define CVATTN_TABLE(NW, WS, MASK, BATCH)                                                            \
-    {CVATTN_V_ROW(NW, WS, T_F32, MASK, BATCH), CVATTN_V_ROW(NW, WS, T_F16, MASK, BATCH),            \
-     CVATTN_V_ROW(NW, WS, T_Q8_0, MASK, BATCH), CVATTN_V_ROW(NW, WS, T_Q4_0, MASK, BATCH),          \
-     CVATTN_V_ROW(NW, WS, T_Q4_1, MASK, BATCH), CVATTN_V_ROW(NW, WS, T_Q5_0, MASK, BATCH),          \
-     CVATTN_V_ROW(NW, WS, T_Q5_1, MASK, BATCH)}
+// Launch table [k type index][v type index]; index order f32 f16 q8_0 q4_0 q4_1 q5_0 q5_1.
+#define CVATTN_V_ROW(KT, MASK, BATCH)                                                                \
+    {launch_rows<KT, T_F32, MASK, BATCH>, launch_rows<KT, T_F16, MASK, BATCH>,                     \
+     launch_rows<KT, T_Q8_0, MASK, BATCH>, launch_rows<KT, T_Q4_0, MASK, BATCH>,                   \
+     launch_rows<KT, T_Q4_1, MASK, BATCH>, launch_rows<KT, T_Q5_0, MASK, BATCH>,                   \
+     launch_rows<KT, T_Q5_1, MASK, BATCH>}
+#define CVATTN_TABLE(MASK, BATCH)                                                                     \
+    {CVATTN_V_ROW(T_F32, MASK, BATCH), CVATTN_V_ROW(T_F16, MASK, BATCH),                           \
+     CVATTN_V_ROW(T_Q8_0, MASK, BATCH), CVATTN_V_ROW(T_Q4_0, MASK, BATCH),                         \
+     CVATTN_V_ROW(T_Q4_1, MASK, BATCH), CVATTN_V_ROW(T_Q5_0, MASK, BATCH),                         \
+     CVATTN_V_ROW(T_Q5_1, MASK, BATCH)}
 
 } // namespace cvattn
