@@ -17,7 +17,20 @@ using namespace cvattn;
 
 namespace {
 
-constexpr int kTargetUnits = 512;  // ~2 workgroups per CU on a 256-CU MI355X
+constexpr int kRowsPerCu = 2; // resident row-tiled workgroups per CU (register bound)
+
+// Compute units of the current device (256 on MI355X), cached per device.
+int cu_count() {
+    static int cached[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
 constexpr size_t kAlign = 256;
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -111,10 +124,18 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
         len = (int)wlen * sh.ks.nw;
     } else {
+        // Split only when the row groups leave most resident workgroup slots idle: every
+        // split writes (and the merge reads back) a full-size fp32 partial of its rows, which
+        // costs more than a partly idle last round of workgroups (DiT at T=1500 measured).
         const int min_split = 256;
         const int64_t base = std::max<int64_t>(1, work);
-        int want = (int)std::max<int64_t>(1, (kTargetUnits + base - 1) / base);
-        want = std::min(want, std::max(1, (n_kv + min_split - 1) / min_split));
+        const int64_t slots = kRowsPerCu * cu_count();
+        int want = 1;
+        if (2 * base < slots) {
+            want = (int)((slots + base - 1) / base);
+            want = std::min(want, std::max(1, (n_kv + min_split - 1) / min_split));
+            want = std::min(want, sh.ks.max_splits);
+        }
         len = (n_kv + want - 1) / want;
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
     }

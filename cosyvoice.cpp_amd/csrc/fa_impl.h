@@ -4,9 +4,10 @@
 // attention kernels share (problem lookup, workgroup decomposition, split merges).
 //
 // Rows.  For one (batch b, kv head kh) the rows are the n_q * G query rows sharing kh
-// (G = H / H_kv), ordered r = i * G + g (query i, q head kh*G + g).  A wave owns 16 rows: the 16
-// columns of its MFMA tiles.  A workgroup is 4 waves (64 rows) sharing 64-token K/V tiles that
-// are staged once per step into LDS, double-buffered: while the waves compute tile s, the
+// (G = H / H_kv), ordered r = i * G + g (query i, q head kh*G + g).  A wave owns two sets of 16
+// rows (the 16 columns of its MFMA tiles), so each K or V operand read from LDS feeds two MFMAs.
+// A workgroup is 4 waves (128 rows) sharing 64-token K/V tiles that are staged once per step
+// into LDS, double-buffered: while the waves compute tile s, the
 // tile s+1 is unpacked into the other buffer from registers loaded two steps ahead, so a step
 // has one barrier.
 //
@@ -33,10 +34,11 @@
 
 namespace cvattn {
 
-constexpr int ROWS_NW = 4;          // waves (16 rows each) per workgroup
+constexpr int ROWS_NW = 4;          // waves per workgroup
+constexpr int ROWS_SETS = 2;        // 16-row sets per wave (sharing every K and V operand read)
 constexpr int ROWS_TS = 64;         // tokens per staged tile
 constexpr int ROWS_RS = 72;         // halfs per LDS tile row (64 dims + pad)
-constexpr int ROWS_ROWS = 16 * ROWS_NW;
+constexpr int ROWS_ROWS = 16 * ROWS_SETS * ROWS_NW;
 constexpr float ROWS_RESCALE_LOG2 = 8.0f;
 // the two K tile buffers double as the split-merge scratch (2 * ROWS * n_splits floats)
 constexpr int ROWS_MERGE_MAX_SPLITS = (2 * ROWS_TS * ROWS_RS * 2 / 4) / (2 * ROWS_ROWS);
@@ -98,20 +100,25 @@ __device__ __forceinline__ UnitPos locate_unit(const FaArgs &args, uint32_t unit
 }
 
 // Last-arriving workgroup of a split row group merges all split partials of its rows
-// (prepared batches: no separate combine launch).  Three phases so the global loads run in
-// parallel: (1) every split's (m, l) of every row into LDS, (2) one thread per row turns them
-// into normalised split weights, (3) each thread sums its outputs over the splits.
-// `scratch` holds 2 * ROWS * n_splits floats (n_splits <= MERGE_MAX_SPLITS).
+// (prepared batches: no separate combine launch).  The partials were written by other
+// workgroups of the same launch and are read with agent-coherent (sc1) vector loads: (1) every
+// split's (m, l) of every row into LDS, (2) one thread per row turns them into normalised split
+// weights, (3) each thread sums 4-dim chunks of its rows over the splits, with the loads of 4
+// splits x all its chunks in flight at once.
+// `scratch` holds 2 * ROWS * n_splits floats (n_splits <= ROWS_MERGE_MAX_SPLITS).
 template <int ROWS, int THREADS>
 __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem &P, int bq, int kh, int rg,
                                              int64_t slot0, int tid, float *scratch) {
+    constexpr int SC1 = 16;
     const int ns = P.n_splits;
     float *sm = scratch;             // [ROWS][ns] m, then normalised weights
     float *sl = scratch + ROWS * ns; // [ROWS][ns] l
-    for (int idx = tid; idx < ROWS * ns; idx += THREADS) {
-        const float *ps = U.partials + (slot0 + idx) * PART_STRIDE; // slot0 + r*ns + s == slot0 + idx
-        sm[idx] = ld_agent(ps + 64);
-        sl[idx] = ld_agent(ps + 65);
+    const __amdgpu_buffer_rsrc_t rp =
+        make_rsrc((gu8 *)(U.partials + slot0 * PART_STRIDE), (int64_t)ROWS * ns * PART_STRIDE * 4);
+    for (int idx = tid; idx < ROWS * ns; idx += THREADS) { // slot0 + r*ns + s == slot0 + idx
+        const u2 ml = __builtin_amdgcn_raw_buffer_load_b64(rp, (idx * PART_STRIDE + 64) * 4, 0, SC1);
+        sm[idx] = as_f32(ml[0]);
+        sl[idx] = as_f32(ml[1]);
     }
     __syncthreads();
     if (tid < ROWS) {
@@ -128,26 +135,42 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
         for (int s = 0; s < ns; s++) sm[tid * ns + s] = M != -INFINITY ? sm[tid * ns + s] * inv : 0.0f;
     }
     __syncthreads();
-    constexpr int PER = ROWS * HEAD / THREADS; // outputs per thread
-    static_assert(PER * THREADS == ROWS * HEAD, "merge tiling");
+    constexpr int PER = ROWS * (HEAD / 4) / THREADS; // 4-dim chunks per thread
+    static_assert(PER * THREADS == ROWS * (HEAD / 4), "merge tiling");
+    f4 acc[PER];
+#pragma unroll
+    for (int e = 0; e < PER; e++) acc[e] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s0 = 0; s0 < ns; s0 += 4) {
+        u4 ov[PER][4];
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            const int c = tid + e * THREADS, r = c >> 4, d0 = (c & 15) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (s0 + j < ns)
+                    ov[e][j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((r * ns + s0 + j) * PART_STRIDE + d0) * 4, 0, SC1);
+        }
+#pragma unroll
+        for (int e = 0; e < PER; e++) {
+            const int r = (tid + e * THREADS) >> 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (s0 + j < ns) acc[e] += as_f4(ov[e][j]) * sm[r * ns + s0 + j];
+        }
+    }
 #pragma unroll
     for (int e = 0; e < PER; e++) {
-        const int idx = tid + e * THREADS;
-        const int r = idx / HEAD, d = idx % HEAD;
+        const int c = tid + e * THREADS, r = c >> 4, d0 = (c & 15) * 4;
         const int row = rg * ROWS + r;
         if (row >= U.n_rows) continue;
-        const float *part = U.partials + (slot0 + (int64_t)r * ns) * PART_STRIDE + d;
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int s = 0; s < ns; s++) acc += sm[r * ns + s] * ld_agent(part + (int64_t)s * PART_STRIDE);
         const int iq = row / U.G, hq = kh * U.G + row % U.G;
-        P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d] = acc;
+        *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc[e];
     }
 }
 
 template <int KT, int VT, bool MASK, bool BATCH>
 __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
-    constexpr int TS = ROWS_TS, RS = ROWS_RS, NTILE = TS / 16, NKB = TS / 32;
+    constexpr int TS = ROWS_TS, RS = ROWS_RS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][TS * RS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[2][TS * RS];
@@ -185,64 +208,72 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         else
             blk_load<VT>(rsrc, voff, t0 * nb1, r);
     };
-
-    // ---- this lane's query row and its Q operand (B of the S^T MFMA) ----
-    const int row = rg * ROWS_ROWS + wv * 16 + col;
-    const bool row_ok = row < U.n_rows;
-    const int iq = row_ok ? row / U.G : 0;
-    const int hq = kh * U.G + (row_ok ? row % U.G : 0);
-
     if (nsteps > 0) load_tile(t_begin, R0);
     if (nsteps > 1) load_tile(t_begin + TS, R1);
 
-    h8 qhi[2], qlo[2];
-    float qsum[2];
+    // ---- this lane's query rows (one per 16-row set) and their Q operands ----
+    int row[NR], iq[NR], hq[NR];
+    bool row_ok[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        row[r] = rg * ROWS_ROWS + wv * (16 * NR) + 16 * r + col;
+        row_ok[r] = row[r] < U.n_rows;
+        iq[r] = row_ok[r] ? row[r] / U.G : 0;
+        hq[r] = kh * U.G + (row_ok[r] ? row[r] % U.G : 0);
+    }
+    h8 qhi[NR][2], qlo[NR][2];
+    float qsum[NR][2];
     float smul; // multiplies the staged K scales / raw scores into base-2 logits
     bool need_lo;
     {
-        gu8 *qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)bq * P.q_nb3;
-        float x[2][8];
-        if (U.q_f16) { // uniform
+        float x[NR][2][8];
 #pragma unroll
-            for (int b = 0; b < 2; b++)
+        for (int r = 0; r < NR; r++) {
+            gu8 *qp = gptr(P.q) + (int64_t)iq[r] * P.q_nb1 + (int64_t)hq[r] * P.q_nb2 + (int64_t)bq * P.q_nb3;
+            if (U.q_f16) { // uniform
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[b][j] = ldg_half(qp + 2 * (32 * b + 8 * g + j));
-        } else {
+                for (int b = 0; b < 2; b++)
 #pragma unroll
-            for (int b = 0; b < 2; b++)
+                    for (int j = 0; j < 8; j++) x[r][b][j] = ldg_half(qp + 2 * (32 * b + 8 * g + j));
+            } else {
 #pragma unroll
-                for (int j = 0; j < 8; j++) x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) x[r][b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
+            }
         }
-        // Q*scale exact in fp16 for every row of the workgroup?
+        // Q*scale exact in fp16 (up to fp16 subnormal rounding, below 2^-24) for every row?
         bool inexact = false;
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int r = 0; r < NR; r++)
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float xs = row_ok ? x[b][j] * U.scale : 0.0f;
-                inexact |= (float)(_Float16)xs != xs;
-            }
+            for (int b = 0; b < 2; b++)
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float xs = row_ok[r] ? x[r][b][j] * U.scale : 0.0f;
+                    inexact |= fabsf((float)(_Float16)xs - xs) > 0x1p-25f;
+                }
         need_lo = __syncthreads_or(inexact) != 0;
         const float qmul = need_lo ? U.scale_log2 : U.scale;
         smul = need_lo ? 1.0f : 1.4426950408889634f;
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            float s = 0.0f;
+        for (int r = 0; r < NR; r++)
 #pragma unroll
-            for (int j = 0; j < 8; j++) {
-                const float xs = row_ok ? x[b][j] * qmul : 0.0f;
-                const _Float16 hx = (_Float16)xs;
-                const _Float16 lx = (_Float16)(xs - (float)hx);
-                qhi[b][j] = hx;
-                qlo[b][j] = lx;
-                s += (float)hx + (float)lx;
+            for (int b = 0; b < 2; b++) {
+                float sm = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    const float xs = row_ok[r] ? x[r][b][j] * qmul : 0.0f;
+                    const _Float16 hx = (_Float16)xs;
+                    const _Float16 lx = (_Float16)(xs - (float)hx);
+                    qhi[r][b][j] = hx;
+                    qlo[r][b][j] = lx;
+                    sm += (float)hx + (need_lo ? (float)lx : 0.0f);
+                }
+                qsum[r][b] = wave_sum16x4(sm);
             }
-            qsum[b] = wave_sum16x4(s);
-        }
     }
     constexpr float kbias = stage_bias<KT>();
-    const f4 cinit0 = {-kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0]};
-    const f4 cinit1 = {-kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1]};
 
     // unpack a staged tile's blocks into LDS buffer `buf`
     auto write_tile = [&](const RawBuf<W> &r, int buf) {
@@ -260,140 +291,157 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         }
     };
 
-    gu8 *mrow = nullptr;
-    if constexpr (MASK)
-        mrow = gptr(P.mask) + (int64_t)iq * P.m_nb1 + (int64_t)(hq % P.m_ne2) * P.m_nb2 +
-               (int64_t)(bq % P.m_ne3) * P.m_nb3;
-
-    float m_ref = -INFINITY; // reference maximum (base 2) of this lane's row
-    float l_run = 0.0f;
-    float corr[2] = {0.0f, 0.0f};
-    f4 oacc[4];
+    gu8 *mrow[NR];
 #pragma unroll
-    for (int i = 0; i < 4; i++) oacc[i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int r = 0; r < NR; r++)
+        mrow[r] = MASK ? gptr(P.mask) + (int64_t)iq[r] * P.m_nb1 + (int64_t)(hq[r] % P.m_ne2) * P.m_nb2 +
+                             (int64_t)(bq % P.m_ne3) * P.m_nb3
+                       : nullptr;
 
-    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS)
+    float m_ref[NR], l_run[NR], corr[NR][2];
+    f4 oacc[NR][4];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        m_ref[r] = -INFINITY; // reference maximum (base 2) of this lane's row
+        l_run[r] = 0.0f;
+        corr[r][0] = corr[r][1] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) oacc[r][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS) for both row sets
     auto compute_tile = [&](int buf, int t0) {
         const _Float16 *cK = sK[buf];
         const _Float16 *cV = sV[buf];
         float(*cS)[2][TS] = sS[buf];
-        f4 s[NTILE];
+        f4 s[NR][NTILE];
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
             const h8 a0 = *(const h8 *)&cK[(16 * tt + col) * RS + 8 * g];
             const h8 a1 = *(const h8 *)&cK[(16 * tt + col) * RS + 32 + 8 * g];
-            if constexpr (!is_quant(KT)) {
-                // no block scales: one accumulator chain over both halves (its init is 0)
-                f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], acc, 0, 0, 0);
-                if (need_lo) {
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[0], acc, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const f4 ci0 = {-kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0]};
+                if constexpr (!is_quant(KT)) {
+                    // no block scales: one accumulator chain over both halves (its init is 0)
+                    f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], acc, 0, 0, 0);
+                    if (need_lo) {
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc, 0, 0, 0);
+                    }
+                    s[r][tt] = acc;
+                } else {
+                    const f4 ci1 = {-kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1]};
+                    f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], ci0, 0, 0, 0);
+                    f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], ci1, 0, 0, 0);
+                    if (need_lo) {
+                        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc0, 0, 0, 0);
+                        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc1, 0, 0, 0);
+                    }
+                    const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
+                    const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
+                    f4 v = d0 * acc0 + d1 * acc1;
+                    if constexpr (has_min(KT)) {
+                        const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
+                        const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
+                        v += m0 * qsum[r][0] + m1 * qsum[r][1];
+                    }
+                    s[r][tt] = v;
                 }
-                s[tt] = acc;
-                continue;
-            }
-            f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[0], cinit0, 0, 0, 0);
-            f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[1], cinit1, 0, 0, 0);
-            if (need_lo) {
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[0], acc0, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[1], acc1, 0, 0, 0);
-            }
-            if constexpr (is_quant(KT)) {
-                const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
-                const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
-                f4 v = d0 * acc0 + d1 * acc1;
-                if constexpr (has_min(KT)) {
-                    const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
-                    const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
-                    v += m0 * qsum[0] + m1 * qsum[1];
-                }
-                s[tt] = v;
             }
         }
         // scores so far are base-2 logits divided by sm2 (quantized K has smul folded into its
         // scales); the mask path turns them into base-2 logits here, the others in the exponent
-        float sm2 = is_quant(KT) ? 1.0f : smul;
-
-        // ---- mask, bounds, softmax with a lazily raised reference maximum ----
-        float mx = -INFINITY;
+        float sm2 = is_quant(KT) || MASK ? 1.0f : smul;
+        const float mmul = is_quant(KT) ? 1.0f : smul;
         const bool full = t0 + TS <= t_end; // uniform
+        h8 pb[NR][NKB][2];
 #pragma unroll
-        for (int tt = 0; tt < NTILE; tt++) {
-            const int tb = t0 + 16 * tt + 4 * g;
-            if constexpr (MASK) {
-                if (full) {
-                    const u2 mw = ldg_u64(mrow + (int64_t)tb * 2);
-                    const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
-                    s[tt][0] = s[tt][0] * sm2 + (float)a[0] * 1.4426950408889634f;
-                    s[tt][1] = s[tt][1] * sm2 + (float)a[1] * 1.4426950408889634f;
-                    s[tt][2] = s[tt][2] * sm2 + (float)c2[0] * 1.4426950408889634f;
-                    s[tt][3] = s[tt][3] * sm2 + (float)c2[1] * 1.4426950408889634f;
-                } else {
+        for (int r = 0; r < NR; r++) {
+            // ---- mask, bounds, softmax with a lazily raised reference maximum ----
+            float mx = -INFINITY;
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
-                        const int t = tb + j;
-                        const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
-                        s[tt][j] = t < t_end ? s[tt][j] * sm2 + mv * 1.4426950408889634f : -INFINITY;
+            for (int tt = 0; tt < NTILE; tt++) {
+                const int tb = t0 + 16 * tt + 4 * g;
+                if constexpr (MASK) {
+                    if (full) {
+                        const u2 mw = ldg_u64(mrow[r] + (int64_t)tb * 2);
+                        const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
+                        s[r][tt][0] = s[r][tt][0] * mmul + (float)a[0] * 1.4426950408889634f;
+                        s[r][tt][1] = s[r][tt][1] * mmul + (float)a[1] * 1.4426950408889634f;
+                        s[r][tt][2] = s[r][tt][2] * mmul + (float)c2[0] * 1.4426950408889634f;
+                        s[r][tt][3] = s[r][tt][3] * mmul + (float)c2[1] * 1.4426950408889634f;
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int t = tb + j;
+                            const float mv = ldg_half(mrow[r] + (int64_t)min(t, P.n_kv - 1) * 2);
+                            s[r][tt][j] = t < t_end ? s[r][tt][j] * mmul + mv * 1.4426950408889634f : -INFINITY;
+                        }
                     }
+                } else if (!full) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        if (tb + j >= t_end) s[r][tt][j] = -INFINITY;
                 }
-            } else if (!full) {
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (tb + j >= t_end) s[tt][j] = -INFINITY;
+                for (int j = 0; j < 4; j++) mx = fmaxf(mx, s[r][tt][j]);
             }
+            mx = wave_max16x4(mx) * sm2;
+            const bool raise = mx > m_ref[r] + ROWS_RESCALE_LOG2;
+            const float m_new = raise ? mx : m_ref[r];
+            if (__builtin_amdgcn_ballot_w64(raise && m_ref[r] != -INFINITY)) { // uniform
+                const float alpha = fast_exp2(m_ref[r] - m_new);
+                l_run[r] *= alpha;
+                corr[r][0] *= alpha;
+                corr[r][1] *= alpha;
 #pragma unroll
-            for (int j = 0; j < 4; j++) mx = fmaxf(mx, s[tt][j]);
-        }
-        if constexpr (MASK) sm2 = 1.0f;
-        mx = wave_max16x4(mx) * sm2;
-        const bool raise = mx > m_ref + ROWS_RESCALE_LOG2;
-        const float m_new = raise ? mx : m_ref;
-        if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
-            const float alpha = fast_exp2(m_ref - m_new);
-            l_run *= alpha;
-            corr[0] *= alpha;
-            corr[1] *= alpha;
-#pragma unroll
-            for (int i = 0; i < 4; i++) oacc[i] *= alpha;
-        }
-        m_ref = m_new;
-        const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
-#pragma unroll
-        for (int tt = 0; tt < NTILE; tt++)
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float p = fast_exp2(__builtin_fmaf(s[tt][j], sm2, -m_use));
-                s[tt][j] = p;
-                l_run += p;
+                for (int i = 0; i < 4; i++) oacc[r][i] *= alpha;
             }
-
-        // ---- O^T += V^T P^T (32 tokens per MFMA: tiles 2kb and 2kb+1) ----
+            m_ref[r] = m_new;
+            const float m_use = m_ref[r] == -INFINITY ? 0.0f : m_ref[r];
 #pragma unroll
-        for (int kb = 0; kb < NKB; kb++) {
-            const f4 plo = s[2 * kb], phi = s[2 * kb + 1];
-            h8 pb[2];
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                f4 xlo = plo, xhi = phi;
-                if constexpr (is_quant(VT)) {
-                    xlo = plo * *(const f4 *)&cS[2][b][32 * kb + 4 * g];
-                    xhi = phi * *(const f4 *)&cS[2][b][32 * kb + 16 + 4 * g];
-                }
+            for (int tt = 0; tt < NTILE; tt++)
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
-                    pb[b][j] = (_Float16)xlo[j];
-                    pb[b][4 + j] = (_Float16)xhi[j];
+                    const float p = fast_exp2(__builtin_fmaf(s[r][tt][j], sm2, -m_use));
+                    s[r][tt][j] = p;
+                    l_run[r] += p;
                 }
-                if constexpr (has_min(VT)) {
-                    const f4 mlo = *(const f4 *)&cS[3][b][32 * kb + 4 * g];
-                    const f4 mhi = *(const f4 *)&cS[3][b][32 * kb + 16 + 4 * g];
-                    const f4 t = plo * mlo + phi * mhi;
-                    corr[b] += t[0] + t[1] + t[2] + t[3];
+            // P^T operands: 32 tokens (tiles 2kb and 2kb+1) per MFMA, V block scale folded in
+#pragma unroll
+            for (int kb = 0; kb < NKB; kb++) {
+                const f4 plo = s[r][2 * kb], phi = s[r][2 * kb + 1];
+#pragma unroll
+                for (int b = 0; b < 2; b++) {
+                    f4 xlo = plo, xhi = phi;
+                    if constexpr (is_quant(VT)) {
+                        xlo = plo * *(const f4 *)&cS[2][b][32 * kb + 4 * g];
+                        xhi = phi * *(const f4 *)&cS[2][b][32 * kb + 16 + 4 * g];
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        pb[r][kb][b][j] = (_Float16)xlo[j];
+                        pb[r][kb][b][4 + j] = (_Float16)xhi[j];
+                    }
+                    if constexpr (has_min(VT)) {
+                        const f4 mlo = *(const f4 *)&cS[3][b][32 * kb + 4 * g];
+                        const f4 mhi = *(const f4 *)&cS[3][b][32 * kb + 16 + 4 * g];
+                        const f4 t = plo * mlo + phi * mhi;
+                        corr[r][b] += t[0] + t[1] + t[2] + t[3];
+                    }
+                    if constexpr (!is_quant(VT)) {
+                        pb[r][kb][1] = pb[r][kb][0]; // one B operand serves both blocks
+                        break;
+                    }
                 }
-                if constexpr (!is_quant(VT)) break; // one B operand serves both blocks
             }
-            if constexpr (!is_quant(VT)) pb[1] = pb[0];
+        }
+
+        // ---- O^T += V^T P^T: each V^T operand (two ds_read_b64_tr_b16) serves both row sets ----
+#pragma unroll
+        for (int kb = 0; kb < NKB; kb++) {
             const int vrow = 32 * kb + 4 * g + (col >> 2);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -404,7 +452,9 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                     h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
                             (__attribute__((address_space(3))) short4_t *)(va + 16 * RS)));
                 const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                oacc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[i >> 1], oacc[i], 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    oacc[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[r][kb][i >> 1], oacc[r][i], 0, 0, 0);
             }
         }
     };
@@ -437,36 +487,38 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     // ---------------- epilogue ----------------
     // partial slot of (row r of this row group, split s) = slot0 + r * n_splits + s
     const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * ROWS_ROWS * P.n_splits;
-    l_run = wave_sum16x4(l_run);
-    if constexpr (has_min(VT)) {
-        corr[0] = wave_sum16x4(corr[0]);
-        corr[1] = wave_sum16x4(corr[1]);
 #pragma unroll
-        for (int i = 0; i < 4; i++) oacc[i] += corr[i >> 1];
-    }
-    if (row_ok) {
-        if (P.n_splits == 1) {
-            const float inv = l_run > 0.0f ? 1.0f / l_run : 0.0f;
-            float *o = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
+    for (int r = 0; r < NR; r++) {
+        l_run[r] = wave_sum16x4(l_run[r]);
+        if constexpr (has_min(VT)) {
+            corr[r][0] = wave_sum16x4(corr[r][0]);
+            corr[r][1] = wave_sum16x4(corr[r][1]);
 #pragma unroll
-            for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i] * inv;
-        } else {
-            float *o = U.partials + (slot0 + (int64_t)(row - rg * ROWS_ROWS) * P.n_splits + split) * PART_STRIDE;
-            if constexpr (BATCH) {
+            for (int i = 0; i < 4; i++) oacc[r][i] += corr[r][i >> 1];
+        }
+        if (row_ok[r]) {
+            if (P.n_splits == 1) {
+                const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : 0.0f;
+                float *o = P.dst + (((int64_t)bq * U.n_q + iq[r]) * U.H + hq[r]) * HEAD;
 #pragma unroll
-                for (int i = 0; i < 4; i++)
-#pragma unroll
-                    for (int j = 0; j < 4; j++) st_agent(&o[16 * i + 4 * g + j], oacc[i][j]);
-                if (g == 0) {
-                    st_agent(&o[64], m_ref);
-                    st_agent(&o[65], l_run);
-                }
+                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[r][i] * inv;
             } else {
+                const int64_t slot = slot0 + (int64_t)(row[r] - rg * ROWS_ROWS) * P.n_splits + split;
+                float *o = U.partials + slot * PART_STRIDE;
+                if constexpr (BATCH) {
+                    // agent-coherent (sc1) vector stores, the form of agent-scope atomic stores
+                    const __amdgpu_buffer_rsrc_t rp = make_rsrc((gu8 *)o, PART_STRIDE * 4);
 #pragma unroll
-                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[i];
-                if (g == 0) {
-                    o[64] = m_ref;
-                    o[65] = l_run;
+                    for (int i = 0; i < 4; i++)
+                        __builtin_amdgcn_raw_buffer_store_b128(as_u4(oacc[r][i]), rp, (16 * i + 4 * g) * 4, 0, 16);
+                    if (g == 0) __builtin_amdgcn_raw_buffer_store_b64(u2{as_u32(m_ref[r]), as_u32(l_run[r])}, rp, 64 * 4, 0, 16);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[r][i];
+                    if (g == 0) {
+                        o[64] = m_ref[r];
+                        o[65] = l_run[r];
+                    }
                 }
             }
         }
