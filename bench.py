@@ -142,6 +142,120 @@ def bench_dit(lib, cvattn, torch, dev, iters=50):
     return {"ms_per_layer_call": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flop_per_call": flops, "calls": n}
 
 
+def bench_prefill(lib, cvattn, torch, dev, iters=48):
+    """LLM prefill layer call: 1024 query tokens over 1024 f16 cached tokens, causal mask, 14/2 heads
+    (Q, K, V ~ 0.5 N(0,1)); 24 layers of the same shape are cycled."""
+    nq = nkv = 1024
+    row = HKV * D * 2
+    layers = []
+    for _ in range(L):
+        kc = (0.5 * torch.randn((nkv, HKV * D), device=dev)).half()
+        vc = (0.5 * torch.randn((nkv, HKV * D), device=dev)).half()
+        q = 0.5 * torch.randn((nq, H, D), device=dev)
+        layers.append((kc, vc, q))
+    i = torch.arange(nq, device=dev).view(-1, 1)
+    j = torch.arange(nkv, device=dev).view(1, -1)
+    mask = torch.where(j <= nkv - nq + i, 0.0, float("-inf")).half().contiguous()
+    out = torch.empty((nq, H, D), device=dev, dtype=torch.float32)
+    keep = []
+    plans = []
+    for kc, vc, q in layers:
+        p = cvattn.FaProblem()
+        p.q = cvattn.llm_q_view(q.data_ptr(), D, H, nq)
+        p.k = cvattn.llm_kv_view(kc.data_ptr(), cvattn.F16, D, HKV, nkv, nkv)
+        p.v = cvattn.llm_kv_view(vc.data_ptr(), cvattn.F16, D, HKV, nkv, nkv)
+        p.mask = cvattn.mask_view(mask.data_ptr(), nkv, nq)
+        p.dst = cvattn.out_view(out.data_ptr(), D, H, nq)
+        plans.append(make_plan(lib, cvattn, torch, dev, [p], keep))
+
+    def launch(s):
+        for pl in plans:
+            assert lib.fa_batch_launch(pl, s) == cvattn.OK
+
+    ms, n = time_graph(torch, launch, L, iters, L)
+    visible = sum(nkv - nq + ii + 1 for ii in range(nq))
+    flops = 4.0 * D * H * visible
+    return {"workload": "LLM prefill layer call, 1024 query tokens, causal mask, 1024 f16 cached tokens, 14/2 heads",
+            "us_per_layer_call": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
+            "mfma_frac": flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS}
+
+
+def bench_dit_stream(lib, cvattn, torch, dev, iters=220):
+    """Flow-DiT streaming call: a 50-frame query chunk over a cached 1000-frame prefix plus itself
+    (n_kv 1050), batch 2, 16 heads, f16 cache views; 22 layers' caches are cycled."""
+    nq, nkv, B, HD, NL = 50, 1050, 2, 16, 22
+    caches = []
+    for _ in range(NL):
+        k = torch.randn((B, nkv, HD * D), device=dev).half()
+        v = torch.randn((B, nkv, HD * D), device=dev).half()
+        caches.append((k, v))
+    q = torch.randn((B, nq, HD * D), device=dev)
+    out = torch.empty((B, nq, HD, D), device=dev, dtype=torch.float32)
+    keep, plans = [], []
+    for k, v in caches:
+        p = cvattn.FaProblem()
+        p.q = cvattn.dit_view(q.data_ptr(), nq, B)
+        p.k = cvattn.dit_view(k.data_ptr(), nkv, B, ttype=cvattn.F16)
+        p.v = cvattn.dit_view(v.data_ptr(), nkv, B, ttype=cvattn.F16)
+        p.dst = cvattn.out_view(out.data_ptr(), D, HD, nq, B)
+        plans.append(make_plan(lib, cvattn, torch, dev, [p], keep))
+
+    def launch(s):
+        for pl in plans:
+            assert lib.fa_batch_launch(pl, s) == cvattn.OK
+
+    ms, n = time_graph(torch, launch, NL, iters, NL)
+    nbytes = 2 * B * nkv * HD * D * 2 + 2 * B * nq * HD * D * 4
+    return {"workload": "flow-DiT streaming call, 50-frame chunk over 1000 cached + 50 frames, batch 2, 16 heads, f16 cache",
+            "us_per_layer_call": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
+            "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+
+
+def bench_serving(lib, cvattn, torch, dev, iters=96):
+    """Concurrent-serving decode: 16 sequences x 24 layers, K = V = q8_0, kv_len ~ U{256..8192} (seeded),
+    one query token per sequence; a step is 24 launches, one prepared 16-problem batch per layer."""
+    import numpy as np
+
+    nseq = 16
+    lens = np.random.default_rng(20261201).integers(256, 8193, nseq)
+    rk = cvattn.row_bytes(cvattn.Q8_0, HKV * D)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    keep, plans = [], []
+    total = 0
+    for layer in range(L):
+        probs = []
+        for s_ in range(nseq):
+            n = int(lens[s_])
+            # random bytes are valid q8_0 blocks once each block's fp16 scale is made finite and small
+            kc = torch.randint(0, 256, (n, rk), dtype=torch.uint8, device=dev, generator=gen)
+            vc = torch.randint(0, 256, (n, rk), dtype=torch.uint8, device=dev, generator=gen)
+            for t_ in (kc, vc):
+                t_.view(n, rk // 34, 34)[:, :, 1] = 0x20
+            q = torch.randn((H, D), device=dev)
+            out = torch.empty((H, D), device=dev, dtype=torch.float32)
+            keep += [kc, vc, q, out]
+            p = cvattn.FaProblem()
+            p.q = cvattn.llm_q_view(q.data_ptr(), D, H, 1)
+            p.k = cvattn.llm_kv_view(kc.data_ptr(), cvattn.Q8_0, D, HKV, n, n)
+            p.v = cvattn.llm_kv_view(vc.data_ptr(), cvattn.Q8_0, D, HKV, n, n)
+            p.dst = cvattn.out_view(out.data_ptr(), D, H, 1)
+            probs.append(p)
+            total += n * HKV * 2 * (34 + 34) + 2 * H * D * 4
+        plans.append(make_plan(lib, cvattn, torch, dev, probs, keep))
+
+    def launch(s):
+        for pl in plans:
+            assert lib.fa_batch_launch(pl, s) == cvattn.OK
+
+    ms, n = time_graph(torch, launch, L, iters, L)
+    step_ms = ms * L
+    return {"workload": "serving decode, 16 sequences x 24 layers, q8_0 K and V, ragged kv_len U{256..8192}, "
+                        "one launch per layer", "kv_lens": [int(x) for x in lens],
+            "us_per_step": step_ms * 1e3, "gbs": total / (step_ms * 1e-3) / 1e9,
+            "hbm_frac": total / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "bytes_per_step": total}
+
+
 def cpu_baseline(kbuf, vbuf, q, budget_s=12.0):
     """ggml CPU flash-attention loop (restated in oracle/) on copy 0 of the decode workload."""
     import numpy as np
@@ -196,6 +310,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=260)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-dit", action="store_true", help="skip the DiT leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the prefill, DiT-stream and serving legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 256 MiB device copies (reference kernels for the HBM counters)")
     args = ap.parse_args()
@@ -257,6 +372,17 @@ def main():
     dit = None if args.no_dit else bench_dit(lib, cvattn, torch, dev)
     if dit:
         log(f"dit T=1500: {dit['ms_per_layer_call'] * 1e3:.1f} us/call, {dit['tflops']:.1f} TFLOP/s")
+    extra = {}
+    if not args.no_extra:
+        extra["prefill_attn"] = bench_prefill(lib, cvattn, torch, dev)
+        log(f"prefill 1024 causal: {extra['prefill_attn']['us_per_layer_call']:.1f} us/layer, "
+            f"{extra['prefill_attn']['tflops']:.1f} TFLOP/s")
+        extra["dit_stream_attn"] = bench_dit_stream(lib, cvattn, torch, dev)
+        log(f"dit stream 50x1050: {extra['dit_stream_attn']['us_per_layer_call']:.1f} us/call, "
+            f"{extra['dit_stream_attn']['gbs']:.0f} GB/s")
+        extra["serving_decode_attn"] = bench_serving(lib, cvattn, torch, dev)
+        log(f"serving 16x24 ragged q8_0: {extra['serving_decode_attn']['us_per_step']:.1f} us/step, "
+            f"{extra['serving_decode_attn']['gbs']:.0f} GB/s")
 
     cpu = None
     if not args.no_cpu:
@@ -301,6 +427,7 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    res.update(extra)
     print(json.dumps(res))
 
 

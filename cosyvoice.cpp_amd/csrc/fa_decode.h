@@ -152,17 +152,6 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int kvoff = lt * (int)P.k_nb1 + (HP == 2 ? ls * (int)P.k_nb2 : 0) + lb * dblk_bytes<KT>();
     const int vvoff = lt * (int)P.v_nb1 + (HP == 2 ? ls * (int)P.v_nb2 : 0) + lb * dblk_bytes<VT>();
 
-    // issue the first PD steps' loads before anything else
-    RawBuf<blk_words<KT>()> RK[PD];
-    RawBuf<blk_words<VT>()> RV[PD];
-#pragma unroll
-    for (int p = 0; p < PD; p++) {
-        if (p < nsteps) {
-            blk_load<KT>(rk, kvoff, (w_begin + p * TS) * (int)P.k_nb1, RK[p]);
-            blk_load<VT>(rv, vvoff, (w_begin + p * TS) * (int)P.v_nb1, RV[p]);
-        }
-    }
-
     // ---- this lane's query row (MFMA column `col`) and its Q operand (hi + lo fp16) ----
     int iq, hq;
     const bool row_ok = dec_row<HP>(U, khg, rg, col, iq, hq);
@@ -170,6 +159,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     h8 qhi[2], qlo[2];
     float qsum[2];
     bool need_lo = false;
+    RawBuf<blk_words<KT>()> RK[PD];
+    RawBuf<blk_words<VT>()> RV[PD];
     {
         gu8 *qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)bq * P.q_nb3;
         float x[2][8];
@@ -184,6 +175,16 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
                 for (int j = 0; j < 8; j++) x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
         }
+        // the K/V loads go out right behind Q, so the Q conversion below overlaps their latency
+        // (memory results return in issue order)
+#pragma unroll
+        for (int p = 0; p < PD; p++) {
+            if (p < nsteps) {
+                blk_load<KT>(rk, kvoff, (w_begin + p * TS) * (int)P.k_nb1, RK[p]);
+                blk_load<VT>(rv, vvoff, (w_begin + p * TS) * (int)P.v_nb1, RV[p]);
+            }
+        }
+
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             float s = 0.0f;
