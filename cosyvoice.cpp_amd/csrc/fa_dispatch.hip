@@ -24,10 +24,11 @@ static int type_index(int t) {
 
 FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask) {
     FaKernelShape s;
-    // decode-shaped kernel (fa_decode.h): <= 16 rows per kv head and K/V views addressable with
-    // 32-bit buffer offsets; kv heads are paired when each has <= 8 rows (the masked variant
-    // keeps one head per workgroup); everything else runs the row-tiled kernel
-    s.wsplit = n_rows <= 16 && small_views;
+    // decode-shaped kernel (fa_decode.h): <= 64 rows per kv head (up to 4 groups of 16, e.g. the
+    // 50 rows of a DiT streaming chunk) and K/V views addressable with 32-bit buffer offsets; kv
+    // heads are paired when each has <= 8 rows (the masked variant keeps one head per
+    // workgroup); everything else runs the row-tiled kernel
+    s.wsplit = n_rows <= 64 && small_views;
     s.hp = s.wsplit && n_rows <= 8 && h_kv % 2 == 0 && !mask ? 2 : 1;
     s.nw = 4;
     s.tstep = s.wsplit ? 32 / s.hp : ROWS_TS;

@@ -314,6 +314,25 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         const _Float16 *cK = sK[buf];
         const _Float16 *cV = sV[buf];
         float(*cS)[2][TS] = sS[buf];
+        const bool full = t0 + TS <= t_end; // uniform
+        // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
+        // causal prefill) contributes nothing; the wave skips it
+        u2 mwv[NR][NTILE];
+        if constexpr (MASK) {
+            if (full) {
+                bool live = false;
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+#pragma unroll
+                    for (int tt = 0; tt < NTILE; tt++) {
+                        mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
+                        // fp16 -inf is 0xfc00; any other half of the four keeps the tile
+                        live |= row_ok[r] && ((mwv[r][tt][0] & 0xffffu) != 0xfc00u || (mwv[r][tt][0] >> 16) != 0xfc00u ||
+                                              (mwv[r][tt][1] & 0xffffu) != 0xfc00u || (mwv[r][tt][1] >> 16) != 0xfc00u);
+                    }
+                if (__builtin_amdgcn_ballot_w64(live) == 0) return; // uniform
+            }
+        }
         f4 s[NR][NTILE];
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
@@ -355,7 +374,6 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         // scales); the mask path turns them into base-2 logits here, the others in the exponent
         float sm2 = is_quant(KT) || MASK ? 1.0f : smul;
         const float mmul = is_quant(KT) ? 1.0f : smul;
-        const bool full = t0 + TS <= t_end; // uniform
         h8 pb[NR][NKB][2];
 #pragma unroll
         for (int r = 0; r < NR; r++) {
@@ -366,7 +384,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 const int tb = t0 + 16 * tt + 4 * g;
                 if constexpr (MASK) {
                     if (full) {
-                        const u2 mw = ldg_u64(mrow[r] + (int64_t)tb * 2);
+                        const u2 mw = mwv[r][tt];
                         const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
                         s[r][tt][0] = s[r][tt][0] * mmul + (float)a[0] * 1.4426950408889634f;
                         s[r][tt][1] = s[r][tt][1] * mmul + (float)a[1] * 1.4426950408889634f;
