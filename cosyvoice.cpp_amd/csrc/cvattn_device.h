@@ -168,16 +168,25 @@ __device__ __forceinline__ constexpr float stage_bias() {
     return is_quant(T) ? (float)(1024 + code_off(T)) : 0.0f;
 }
 
+// Reductions over the four lanes l, l^16, l^32, l^48 that share a row (MFMA column).  They stay
+// in the VALU: v_permlane32_swap exchanges the wave halves of two registers and
+// v_permlane16_swap the odd rows of one with the even rows of the other, so with both operands
+// holding v each lane ends with its own value and its partner's (no LDS round trip).
 __device__ __forceinline__ float wave_max16x4(float v) {
-    // reduce over the four lanes l, l^16, l^32, l^48 that share a row
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    const uint32_t u = as_u32(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(as_f32(a[0]), as_f32(a[1]));
+    const uint32_t w = as_u32(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return fmaxf(as_f32(b[0]), as_f32(b[1]));
 }
 __device__ __forceinline__ float wave_sum16x4(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    const uint32_t u = as_u32(v);
+    const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = as_f32(a[0]) + as_f32(a[1]);
+    const uint32_t w = as_u32(v);
+    const auto b = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    return as_f32(b[0]) + as_f32(b[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }

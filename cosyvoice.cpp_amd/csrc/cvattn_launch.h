@@ -7,7 +7,7 @@
 
 namespace cvattn {
 
-// Workgroup shape chosen for a problem: decode-shaped (<= 16 rows per kv head, waves split the
+// Workgroup shape chosen for a problem: decode-shaped (<= 64 rows per kv head, waves split the
 // tokens) or row-tiled (waves split the rows).
 struct FaKernelShape {
     bool wsplit;        // decode kernel (fa_decode.h)

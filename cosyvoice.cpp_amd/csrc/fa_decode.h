@@ -1,6 +1,7 @@
-// fa_decode.h -- decode-shaped flash attention for gfx950: at most 16 query rows per kv head
-// (GQA decode over the LLM KV cache: the 7 q heads of a Qwen2-0.5B kv head times a few query
-// tokens), the GGML_OP_FLASH_ATTN_EXT node of src/cosyvoice-kv-cache.cpp:383-384 in decode.
+// fa_decode.h -- decode-shaped flash attention for gfx950: at most 64 query rows per kv head, in
+// row groups of 16 (GQA decode over the LLM KV cache: the 7 q heads of a Qwen2-0.5B kv head times
+// a few query tokens, or the 50-row chunk of a DiT streaming step), the GGML_OP_FLASH_ATTN_EXT
+// node of src/cosyvoice-kv-cache.cpp:383-384 in decode.
 //
 // The KV cache is streamed once, in whole ggml blocks.  A workgroup is 4 independent waves on
 // one (batch, kv-head group, token split); each wave walks its own run of tokens in steps of 32

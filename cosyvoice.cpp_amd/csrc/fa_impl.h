@@ -1,6 +1,6 @@
 // fa_impl.h -- flash attention for gfx950 (the GGML_OP_FLASH_ATTN_EXT node of
 // src/cosyvoice-kv-cache.cpp:383-384 and src/cosyvoice-graph.cpp:375-376): the row-tiled kernel
-// for prefill, DiT and every problem with more than 16 query rows per kv head, plus what all
+// for prefill, DiT and every problem with more than 64 query rows per kv head, plus what all
 // attention kernels share (problem lookup, workgroup decomposition, split merges).
 //
 // Rows.  For one (batch b, kv head kh) the rows are the n_q * G query rows sharing kh
@@ -31,6 +31,8 @@
 #include "cvattn_device.h"
 #include "cvattn_launch.h"
 #include "kv_blocks.h"
+
+#include <type_traits>
 
 namespace cvattn {
 
@@ -309,17 +311,18 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         for (int i = 0; i < 4; i++) oacc[r][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS) for both row sets
-    auto compute_tile = [&](int buf, int t0) {
+    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS) for both row sets; `full_c`
+    // (std::true_type) says every token of the tile is in range, so no bounds code is emitted
+    auto compute_tile = [&](int buf, int t0, auto full_c) {
         const _Float16 *cK = sK[buf];
         const _Float16 *cV = sV[buf];
         float(*cS)[2][TS] = sS[buf];
-        const bool full = t0 + TS <= t_end; // uniform
+        constexpr bool full = decltype(full_c)::value;
         // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
         // causal prefill) contributes nothing; the wave skips it
         u2 mwv[NR][NTILE];
         if constexpr (MASK) {
-            if (full) {
+            if constexpr (full) {
                 bool live = false;
 #pragma unroll
                 for (int r = 0; r < NR; r++)
@@ -334,42 +337,55 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
             }
         }
         f4 s[NR][NTILE];
+        // every K operand of the tile is read before the first MFMA (one LDS wait, not four)
+        h8 ka[NTILE][2];
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
-            const h8 a0 = *(const h8 *)&cK[(16 * tt + col) * RS + 8 * g];
-            const h8 a1 = *(const h8 *)&cK[(16 * tt + col) * RS + 32 + 8 * g];
+            ka[tt][0] = *(const h8 *)&cK[(16 * tt + col) * RS + 8 * g];
+            ka[tt][1] = *(const h8 *)&cK[(16 * tt + col) * RS + 32 + 8 * g];
+        }
+        // the lo MFMAs are a uniform choice per launch; each choice is one straight-line block
+        auto qk = [&](auto lo_c) {
+            constexpr bool LO = decltype(lo_c)::value;
 #pragma unroll
-            for (int r = 0; r < NR; r++) {
-                const f4 ci0 = {-kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0]};
-                if constexpr (!is_quant(KT)) {
-                    // no block scales: one accumulator chain over both halves (its init is 0)
-                    f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
-                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], acc, 0, 0, 0);
-                    if (need_lo) {
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc, 0, 0, 0);
-                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc, 0, 0, 0);
+            for (int tt = 0; tt < NTILE; tt++) {
+                const h8 a0 = ka[tt][0];
+                const h8 a1 = ka[tt][1];
+#pragma unroll
+                for (int r = 0; r < NR; r++) {
+                    const f4 ci0 = {-kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0], -kbias * qsum[r][0]};
+                    if constexpr (!is_quant(KT)) {
+                        // no block scales: one accumulator chain over both halves (its init is 0)
+                        f4 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], f4{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], acc, 0, 0, 0);
+                        if constexpr (LO) {
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc, 0, 0, 0);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc, 0, 0, 0);
+                        }
+                        s[r][tt] = acc;
+                    } else {
+                        const f4 ci1 = {-kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1]};
+                        f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], ci0, 0, 0, 0);
+                        f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], ci1, 0, 0, 0);
+                        if constexpr (LO) {
+                            acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc0, 0, 0, 0);
+                            acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc1, 0, 0, 0);
+                        }
+                        const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
+                        const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
+                        f4 v = d0 * acc0 + d1 * acc1;
+                        if constexpr (has_min(KT)) {
+                            const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
+                            const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
+                            v += m0 * qsum[r][0] + m1 * qsum[r][1];
+                        }
+                        s[r][tt] = v;
                     }
-                    s[r][tt] = acc;
-                } else {
-                    const f4 ci1 = {-kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1], -kbias * qsum[r][1]};
-                    f4 acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[r][0], ci0, 0, 0, 0);
-                    f4 acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[r][1], ci1, 0, 0, 0);
-                    if (need_lo) {
-                        acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc0, 0, 0, 0);
-                        acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc1, 0, 0, 0);
-                    }
-                    const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
-                    const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
-                    f4 v = d0 * acc0 + d1 * acc1;
-                    if constexpr (has_min(KT)) {
-                        const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
-                        const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
-                        v += m0 * qsum[r][0] + m1 * qsum[r][1];
-                    }
-                    s[r][tt] = v;
                 }
             }
-        }
+        };
+        if (need_lo) qk(std::true_type{});
+        else qk(std::false_type{});
         // scores so far are base-2 logits divided by sm2 (quantized K has smul folded into its
         // scales); the mask path turns them into base-2 logits here, the others in the exponent
         float sm2 = is_quant(KT) || MASK ? 1.0f : smul;
@@ -383,7 +399,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
             for (int tt = 0; tt < NTILE; tt++) {
                 const int tb = t0 + 16 * tt + 4 * g;
                 if constexpr (MASK) {
-                    if (full) {
+                    if constexpr (full) {
                         const u2 mw = mwv[r][tt];
                         const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
                         s[r][tt][0] = s[r][tt][0] * mmul + (float)a[0] * 1.4426950408889634f;
@@ -398,7 +414,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                             s[r][tt][j] = t < t_end ? s[r][tt][j] * mmul + mv * 1.4426950408889634f : -INFINITY;
                         }
                     }
-                } else if (!full) {
+                } else if constexpr (!full) {
 #pragma unroll
                     for (int j = 0; j < 4; j++)
                         if (tb + j >= t_end) s[r][tt][j] = -INFINITY;
@@ -425,7 +441,9 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 for (int j = 0; j < 4; j++) {
                     const float p = fast_exp2(__builtin_fmaf(s[r][tt][j], sm2, -m_use));
                     s[r][tt][j] = p;
-                    l_run[r] += p;
+                    // with quantized V the row sum is taken here; otherwise from the fp16 weights
+                    // the PV product uses (v_dot2 over pairs, below)
+                    if constexpr (is_quant(VT)) l_run[r] += p;
                 }
             // P^T operands: 32 tokens (tiles 2kb and 2kb+1) per MFMA, V block scale folded in
 #pragma unroll
@@ -451,6 +469,11 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                     }
                     if constexpr (!is_quant(VT)) {
                         pb[r][kb][1] = pb[r][kb][0]; // one B operand serves both blocks
+                        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+                        for (int j = 0; j < 8; j += 2)
+                            l_run[r] = __builtin_amdgcn_fdot2(h2{pb[r][kb][0][j], pb[r][kb][0][j + 1]}, one,
+                                                              l_run[r], false);
                         break;
                     }
                 }
@@ -484,23 +507,27 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         if (nsteps > 2) load_tile(t_begin + 2 * TS, R0);
     }
     __syncthreads();
-    for (int s0 = 0; s0 < nsteps; s0 += 2) {
+    // full tiles run in the loop; only the last tile can be partial, and it runs after the loop
+    // from the buffer the loop staged it into
+    const int nfull = max(0, t_end - t_begin) / TS; // uniform
+    for (int s0 = 0; s0 < nfull; s0 += 2) {
         // even step: compute buffer 0, stage tile s0+1 (R1) into buffer 1
-        compute_tile(0, t_begin + s0 * TS);
+        compute_tile(0, t_begin + s0 * TS, std::true_type{});
         if (s0 + 1 < nsteps) {
             write_tile(R1, 1);
             if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TS, R1);
         }
         __syncthreads();
-        if (s0 + 1 >= nsteps) break;
+        if (s0 + 1 >= nfull) break;
         // odd step: compute buffer 1, stage tile s0+2 (R0) into buffer 0
-        compute_tile(1, t_begin + (s0 + 1) * TS);
+        compute_tile(1, t_begin + (s0 + 1) * TS, std::true_type{});
         if (s0 + 2 < nsteps) {
             write_tile(R0, 0);
             if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TS, R0);
         }
         __syncthreads();
     }
+    if (nfull < nsteps) compute_tile(nfull & 1, t_begin + nfull * TS, std::false_type{});
 
     // ---------------- epilogue ----------------
     // partial slot of (row r of this row group, split s) = slot0 + r * n_splits + s
