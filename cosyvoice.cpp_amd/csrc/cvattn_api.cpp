@@ -449,11 +449,8 @@ CVATTN_API int cvattn_supports_set_rows(const cvattn_tensor *dst, const cvattn_t
     return check_set_rows(dst, src, idx) == CVATTN_OK ? 1 : 0;
 }
 
-CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
-                               const cvattn_tensor *idx, cvattn_stream_t stream) {
-    int rc = check_set_rows(dst, src, idx);
-    if (rc) return rc;
-    SetRowsArgs a;
+static void fill_set_rows(SetRowsArgs &a, const cvattn_tensor *dst, const cvattn_tensor *src,
+                          const cvattn_tensor *idx) {
     std::memset(&a, 0, sizeof(a));
     a.dst = (uint8_t *)dst->data;
     a.src = (const uint8_t *)src->data;
@@ -477,6 +474,91 @@ CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *sr
     a.idx_i64 = idx->type == 27 ? 1 : 0;
     const int64_t per = type_block(dst->type) == QK ? QK : 1;
     a.total = (src->ne[0] / per) * src->ne[1] * src->ne[2] * src->ne[3];
+}
+
+CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
+                               const cvattn_tensor *idx, cvattn_stream_t stream) {
+    int rc = check_set_rows(dst, src, idx);
+    if (rc) return rc;
+    SetRowsArgs a;
+    fill_set_rows(a, dst, src, idx);
+    return hip_status(set_rows_launch(dst->type, a, (hipStream_t)stream));
+}
+
+// ---- RoPE ------------------------------------------------------------------------------------
+
+// The rope forms cosyvoice.cpp uses (ggml_rope_ext with no frequency factors, ext_factor 0,
+// attn_factor 1): NORMAL or NEOX, an even n_dims within the rope input.
+static int check_rope_params(int64_t seg, int n_dims, int mode, float freq_base, float freq_scale) {
+    if (mode != CVATTN_ROPE_NORMAL && mode != CVATTN_ROPE_NEOX) return CVATTN_ERR_UNSUPPORTED;
+    if (seg <= 0 || (seg & 1) || n_dims <= 0 || (n_dims & 1) || n_dims > seg) return CVATTN_ERR_BAD_ARGS;
+    if (!(freq_base > 0.0f) || !std::isfinite(freq_base) || !std::isfinite(freq_scale)) return CVATTN_ERR_BAD_ARGS;
+    return CVATTN_OK;
+}
+
+// ggml's CPU rope takes theta_scale from the C library's powf once per op.
+static float rope_theta_scale(float freq_base, int n_dims) { return powf(freq_base, -2.0f / (float)n_dims); }
+
+CVATTN_API int cvattn_rope(const cvattn_tensor *dst, const cvattn_tensor *src, const cvattn_tensor *pos,
+                           int n_dims, int mode, float freq_base, float freq_scale, cvattn_stream_t stream) {
+    if (!dst || !src || !pos) return CVATTN_ERR_BAD_ARGS;
+    if (src->type != T_F32 || dst->type != T_F32 || pos->type != T_I32) return CVATTN_ERR_UNSUPPORTED;
+    if (src->nb[0] != 4 || dst->nb[0] != 4 || pos->nb[0] != 4) return CVATTN_ERR_UNSUPPORTED;
+    for (int i = 0; i < 4; i++)
+        if (src->ne[i] < 0 || dst->ne[i] != src->ne[i]) return CVATTN_ERR_BAD_ARGS;
+    int rc = check_rope_params(src->ne[0], n_dims, mode, freq_base, freq_scale);
+    if (rc) return rc;
+    if (pos->ne[0] != src->ne[2]) return CVATTN_ERR_BAD_ARGS; // ggml_rope_ext: one position per i2
+    const int64_t total = src->ne[0] * src->ne[1] * src->ne[2] * src->ne[3];
+    if (total > 0 && (!dst->data || !src->data || !pos->data)) return CVATTN_ERR_BAD_ARGS;
+    RopeArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.dst = (float *)dst->data;
+    a.src = (const float *)src->data;
+    a.pos = (const int32_t *)pos->data;
+    a.ne0 = src->ne[0];
+    a.ne1 = src->ne[1];
+    a.ne2 = src->ne[2];
+    a.ne3 = src->ne[3];
+    a.src_nb1 = (int64_t)src->nb[1];
+    a.src_nb2 = (int64_t)src->nb[2];
+    a.src_nb3 = (int64_t)src->nb[3];
+    a.dst_nb1 = (int64_t)dst->nb[1];
+    a.dst_nb2 = (int64_t)dst->nb[2];
+    a.dst_nb3 = (int64_t)dst->nb[3];
+    a.rope_dims = n_dims;
+    a.rope_neox = mode == CVATTN_ROPE_NEOX ? 1 : 0;
+    a.theta_scale = rope_theta_scale(freq_base, n_dims);
+    a.freq_scale = freq_scale;
+    a.total = total;
+    return hip_status(rope_launch(a, (hipStream_t)stream));
+}
+
+CVATTN_API int cvattn_rope_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src, const cvattn_tensor *idx,
+                                    const cvattn_tensor *pos, int64_t head, int n_dims, int mode, float freq_base,
+                                    float freq_scale, cvattn_stream_t stream) {
+    int rc = check_set_rows(dst, src, idx);
+    if (rc) return rc;
+    if (!pos) return CVATTN_ERR_BAD_ARGS;
+    if (pos->type != T_I32) return CVATTN_ERR_UNSUPPORTED;
+    rc = check_rope_params(head, n_dims, mode, freq_base, freq_scale);
+    if (rc) return rc;
+    if (src->ne[0] % head) return CVATTN_ERR_BAD_ARGS;
+    // one position per source row, contiguous
+    const int64_t n_pos = pos->ne[0] * pos->ne[1] * pos->ne[2] * pos->ne[3];
+    if (n_pos != src->ne[1] * src->ne[2] * src->ne[3]) return CVATTN_ERR_BAD_ARGS;
+    if (pos->nb[0] != 4 || pos->nb[1] != 4 * (size_t)pos->ne[0] || pos->nb[2] != pos->nb[1] * (size_t)pos->ne[1] ||
+        pos->nb[3] != pos->nb[2] * (size_t)pos->ne[2])
+        return CVATTN_ERR_UNSUPPORTED;
+    if (n_pos > 0 && !pos->data) return CVATTN_ERR_BAD_ARGS;
+    SetRowsArgs a;
+    fill_set_rows(a, dst, src, idx);
+    a.pos = (const int32_t *)pos->data;
+    a.rope_seg = head;
+    a.rope_dims = n_dims;
+    a.rope_neox = mode == CVATTN_ROPE_NEOX ? 1 : 0;
+    a.theta_scale = rope_theta_scale(freq_base, n_dims);
+    a.freq_scale = freq_scale;
     return hip_status(set_rows_launch(dst->type, a, (hipStream_t)stream));
 }
 

@@ -35,7 +35,28 @@ struct SetRowsArgs {
     int64_t idx_ne1, idx_ne2;
     int32_t idx_i64;
     int64_t total;
+    // RoPE in front of the write (rope_dims = 0: plain set_rows)
+    const int32_t *pos;   // one position per source row, flattened (i1, i2, i3)
+    int64_t rope_seg;     // elements per rope input (head)
+    int32_t rope_dims;    // rotated dims per input (even, <= rope_seg)
+    int32_t rope_neox;    // pairing: (k, k + dims/2) instead of (2k, 2k+1)
+    float theta_scale;    // powf(freq_base, -2/dims), taken on the host
+    float freq_scale;
 };
 hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st);
+
+// ggml_rope_ext on f32 tensors [ne0, ne1, ne2, ne3], position pos[i2].
+struct RopeArgs {
+    float *dst;
+    const float *src;
+    const int32_t *pos;
+    int64_t ne0, ne1, ne2, ne3;
+    int64_t src_nb1, src_nb2, src_nb3;
+    int64_t dst_nb1, dst_nb2, dst_nb3;
+    int32_t rope_dims, rope_neox;
+    float theta_scale, freq_scale;
+    int64_t total; // ne0 * ne1 * ne2 * ne3
+};
+hipError_t rope_launch(const RopeArgs &a, hipStream_t st);
 
 } // namespace cvattn

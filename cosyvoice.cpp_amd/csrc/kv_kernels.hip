@@ -2,7 +2,11 @@
 //   * dequantize: the test entry for the in-register unpacking the attention kernels use
 //     (same raw8_load/raw8_unpack path), bit-exact to ggml's dequantize_row_*;
 //   * set_rows: the quantize-on-write KV update of cosyvoice_kv_cache::update_cache
-//     (src/cosyvoice-kv-cache.cpp:316,322), bit-exact to ggml's quantize_row_*_ref.
+//     (src/cosyvoice-kv-cache.cpp:316,322), bit-exact to ggml's quantize_row_*_ref, optionally
+//     with the K rotary embedding of the same layer fused in front (src/cosyvoice-llm.cpp:57,
+//     src/cosyvoice-graph.cpp:352);
+//   * rope: ggml_rope_ext for the query side (src/cosyvoice-llm.cpp:56,
+//     src/cosyvoice-graph.cpp:351).
 #include "cvattn_device.h"
 #include "cvattn_launch.h"
 
@@ -138,7 +142,100 @@ __device__ void quantize_block_ref(const float *x, uint8_t *y) {
     }
 }
 
-template <int T>
+// ------------------------------------------------------------------------------------------
+// RoPE as ggml's CPU backend forms it (ggml_rope_ext, ext_factor 0, attn_factor 1): the angle of
+// pair k is p times theta_scale k times (one float multiply per pair, in order), times
+// freq_scale; cos/sin of that; x0*c - x1*s and x0*s + x1*c rounded product by product.
+// ------------------------------------------------------------------------------------------
+struct RopeAngle {
+    float p, ts, fs, th;
+    int k;  // pair whose angle th holds
+    int kc; // pair whose cos/sin are held
+    float c, s;
+    __device__ void init(float pos, float theta_scale, float freq_scale) {
+        p = pos;
+        ts = theta_scale;
+        fs = freq_scale;
+        th = pos;
+        k = 0;
+        kc = -1;
+    }
+    // walks forward from the last pair asked for (from pair 0 when k goes back)
+    __device__ void at(int kk) {
+        if (kk == kc) return;
+        if (kk < k) {
+            th = p;
+            k = 0;
+        }
+        while (k < kk) {
+            th = th * ts;
+            k++;
+        }
+        sincosf(fs * th, &s, &c);
+        kc = kk;
+    }
+};
+
+// Element i (< seg) of rope(x) for one rope input x[0..seg).
+__device__ __forceinline__ float rope_value(const float *x, int i, int dims, bool neox, RopeAngle &A) {
+#pragma clang fp contract(off)
+    if (i >= dims) return x[i];
+    int k, a, b;
+    bool second;
+    if (neox) {
+        const int half = dims >> 1;
+        second = i >= half;
+        k = second ? i - half : i;
+        a = k;
+        b = k + half;
+    } else {
+        k = i >> 1;
+        a = 2 * k;
+        b = a + 1;
+        second = (i & 1) != 0;
+    }
+    A.at(k);
+    const float x0 = x[a], x1 = x[b];
+    return second ? x0 * A.s + x1 * A.c : x0 * A.c - x1 * A.s;
+}
+
+// One thread per unit of two elements: rotated pair k (k < dims/2), or two copied tail elements.
+// Every element is read and written by one thread, so dst may alias src.
+__global__ __launch_bounds__(256) void rope_kernel(RopeArgs a) {
+#pragma clang fp contract(off)
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t units = a.ne0 >> 1;
+    if (gid >= a.total / 2) return;
+    const int64_t u = gid % units;
+    int64_t r = gid / units;
+    const int64_t i1 = r % a.ne1;
+    r /= a.ne1;
+    const int64_t i2 = r % a.ne2;
+    const int64_t i3 = r / a.ne2;
+    const float *x = (const float *)((const uint8_t *)a.src + i1 * a.src_nb1 + i2 * a.src_nb2 + i3 * a.src_nb3);
+    float *y = (float *)((uint8_t *)a.dst + i1 * a.dst_nb1 + i2 * a.dst_nb2 + i3 * a.dst_nb3);
+    const int half = a.rope_dims >> 1;
+    if (u < half) {
+        const int k = (int)u;
+        const int ia = a.rope_neox ? k : 2 * k;
+        const int ib = a.rope_neox ? k + half : 2 * k + 1;
+        RopeAngle A;
+        A.init((float)a.pos[i2], a.theta_scale, a.freq_scale);
+        A.at(k);
+        const float x0 = x[ia], x1 = x[ib];
+        const float y0 = x0 * A.c - x1 * A.s;
+        const float y1 = x0 * A.s + x1 * A.c;
+        y[ia] = y0;
+        y[ib] = y1;
+    } else {
+        const int64_t i = a.rope_dims + 2 * (u - half);
+        const float x0 = x[i], x1 = x[i + 1];
+        y[i] = x0;
+        y[i + 1] = x1;
+    }
+}
+
+template <int T, bool ROPE>
 __global__ __launch_bounds__(256) void set_rows_kernel(SetRowsArgs a) {
     const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= a.total) return;
@@ -160,15 +257,27 @@ __global__ __launch_bounds__(256) void set_rows_kernel(SetRowsArgs a) {
         i1 = v;
     }
     if (i1 < 0 || i1 >= a.dst_rows) return; // out-of-range positions write nothing
-    const float *x = (const float *)(a.src + i01 * a.src_nb1 + i02 * a.src_nb2 + i03 * a.src_nb3) + e * per;
+    const float *row = (const float *)(a.src + i01 * a.src_nb1 + i02 * a.src_nb2 + i03 * a.src_nb3);
+    const float *x = row + e * per;
     uint8_t *y = a.dst + i1 * a.dst_nb1 + i02 * a.dst_nb2 + i03 * a.dst_nb3 + e * type_bytes(T);
-    if constexpr (T == T_F32) {
-        __builtin_memcpy(y, x, 4);
-    } else if constexpr (T == T_F16) {
-        st_half(y, *x);
+    float xb[per];
+    if constexpr (ROPE) {
+        // the per elements of this unit, rotated within their rope input (head) of the row
+        RopeAngle A;
+        A.init((float)a.pos[i01 + a.n_rows * (i02 + a.ne2 * i03)], a.theta_scale, a.freq_scale);
+        for (int j = 0; j < per; j++) {
+            const int64_t c = e * per + j;
+            const int64_t seg = c / a.rope_seg;
+            xb[j] = rope_value(row + seg * a.rope_seg, (int)(c - seg * a.rope_seg), a.rope_dims, a.rope_neox != 0, A);
+        }
     } else {
-        float xb[32];
-        for (int j = 0; j < 32; j++) xb[j] = x[j];
+        for (int j = 0; j < per; j++) xb[j] = x[j];
+    }
+    if constexpr (T == T_F32) {
+        __builtin_memcpy(y, &xb[0], 4);
+    } else if constexpr (T == T_F16) {
+        st_half(y, xb[0]);
+    } else {
         quantize_block_ref<T>(xb, y);
     }
 }
@@ -203,19 +312,31 @@ hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipS
     return hipGetLastError();
 }
 
-hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st) {
-    if (a.total <= 0) return hipSuccess;
+template <bool ROPE>
+static hipError_t set_rows_launch_t(int type, const SetRowsArgs &a, hipStream_t st) {
     const dim3 grid((unsigned)((a.total + 255) / 256)), block(256);
     switch (type) {
-    case T_F32: hipLaunchKernelGGL(set_rows_kernel<T_F32>, grid, block, 0, st, a); break;
-    case T_F16: hipLaunchKernelGGL(set_rows_kernel<T_F16>, grid, block, 0, st, a); break;
-    case T_Q8_0: hipLaunchKernelGGL(set_rows_kernel<T_Q8_0>, grid, block, 0, st, a); break;
-    case T_Q4_0: hipLaunchKernelGGL(set_rows_kernel<T_Q4_0>, grid, block, 0, st, a); break;
-    case T_Q4_1: hipLaunchKernelGGL(set_rows_kernel<T_Q4_1>, grid, block, 0, st, a); break;
-    case T_Q5_0: hipLaunchKernelGGL(set_rows_kernel<T_Q5_0>, grid, block, 0, st, a); break;
-    case T_Q5_1: hipLaunchKernelGGL(set_rows_kernel<T_Q5_1>, grid, block, 0, st, a); break;
+    case T_F32: hipLaunchKernelGGL((set_rows_kernel<T_F32, ROPE>), grid, block, 0, st, a); break;
+    case T_F16: hipLaunchKernelGGL((set_rows_kernel<T_F16, ROPE>), grid, block, 0, st, a); break;
+    case T_Q8_0: hipLaunchKernelGGL((set_rows_kernel<T_Q8_0, ROPE>), grid, block, 0, st, a); break;
+    case T_Q4_0: hipLaunchKernelGGL((set_rows_kernel<T_Q4_0, ROPE>), grid, block, 0, st, a); break;
+    case T_Q4_1: hipLaunchKernelGGL((set_rows_kernel<T_Q4_1, ROPE>), grid, block, 0, st, a); break;
+    case T_Q5_0: hipLaunchKernelGGL((set_rows_kernel<T_Q5_0, ROPE>), grid, block, 0, st, a); break;
+    case T_Q5_1: hipLaunchKernelGGL((set_rows_kernel<T_Q5_1, ROPE>), grid, block, 0, st, a); break;
     default: return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st) {
+    if (a.total <= 0) return hipSuccess;
+    return a.rope_dims > 0 ? set_rows_launch_t<true>(type, a, st) : set_rows_launch_t<false>(type, a, st);
+}
+
+hipError_t rope_launch(const RopeArgs &a, hipStream_t st) {
+    if (a.total <= 0) return hipSuccess;
+    const int64_t units = a.total / 2;
+    hipLaunchKernelGGL(rope_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0, st, a);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@ BLOCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32}
 TYPE_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34}
 
 OK, ERR_UNSUPPORTED, ERR_BAD_ARGS, ERR_WORKSPACE_TOO_SMALL, ERR_HIP = 0, 1, 2, 3, 4
+ROPE_NORMAL, ROPE_NEOX = 0, 2  # CVATTN_ROPE_* (ggml rope modes)
 PREC_DEFAULT, PREC_F32 = 0, 10
 
 
@@ -160,6 +161,11 @@ class Lib:
         L.cvattn_supports_set_rows.restype = ctypes.c_int
         L.cvattn_set_rows.argtypes = [P, P, P, vp]
         L.cvattn_set_rows.restype = ctypes.c_int
+        L.cvattn_rope.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, vp]
+        L.cvattn_rope.restype = ctypes.c_int
+        L.cvattn_rope_set_rows.argtypes = [P, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+                                           ctypes.c_float, vp]
+        L.cvattn_rope_set_rows.restype = ctypes.c_int
         L.cvattn_status_string.argtypes = [ctypes.c_int]
         L.cvattn_status_string.restype = ctypes.c_char_p
         self.L = L
@@ -211,6 +217,14 @@ class Lib:
     def set_rows(self, dst, src, idx, stream=0) -> int:
         return int(self.L.cvattn_set_rows(self._p(dst), self._p(src), self._p(idx), stream or None))
 
+    def rope(self, dst, src, pos, n_dims, mode, freq_base, freq_scale=1.0, stream=0) -> int:
+        return int(self.L.cvattn_rope(self._p(dst), self._p(src), self._p(pos), n_dims, mode, freq_base, freq_scale,
+                                      stream or None))
+
+    def rope_set_rows(self, dst, src, idx, pos, head, n_dims, mode, freq_base, freq_scale=1.0, stream=0) -> int:
+        return int(self.L.cvattn_rope_set_rows(self._p(dst), self._p(src), self._p(idx), self._p(pos), head, n_dims,
+                                               mode, freq_base, freq_scale, stream or None))
+
     def status_string(self, rc) -> str:
         return self.L.cvattn_status_string(rc).decode()
 
@@ -219,7 +233,7 @@ EXPORTED = [
     "cvattn_supports_flash_attn_ext", "cvattn_flash_attn_ext_workspace", "cvattn_flash_attn_ext",
     "cvattn_fa_batch_workspace", "cvattn_fa_batch_prepare", "cvattn_fa_batch_launch",
     "cvattn_block_size", "cvattn_type_size", "cvattn_dequantize",
-    "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_status_string",
+    "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_rope", "cvattn_rope_set_rows", "cvattn_status_string",
 ]
 
 _lib = None

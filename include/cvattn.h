@@ -159,6 +159,37 @@ CVATTN_API int cvattn_supports_set_rows(const cvattn_tensor *dst, const cvattn_t
 CVATTN_API int cvattn_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
                                const cvattn_tensor *idx, cvattn_stream_t stream);
 
+/* --------------------------------------------------------------------------------------------
+ * Rotary position embedding, ggml_rope_ext with freq_factors NULL, ext_factor 0 and
+ * attn_factor 1 -- the forms cosyvoice.cpp builds:
+ *   src/cosyvoice-llm.cpp:56-57     Q and K of each Qwen2 layer: NEOX, n_dims = head dim (64),
+ *                                   freq_base = rope_theta from the GGUF;
+ *   src/cosyvoice-graph.cpp:351-352 DiT query/key rows [1024, 1, T*B]: ggml_rope NORMAL,
+ *                                   n_dims = 64 (only the first 64 of 1024 dims), base 10000.
+ * Pair k < n_dims/2 is (2k, 2k+1) for NORMAL and (k, k + n_dims/2) for NEOX; its angle is
+ * p * s^k * freq_scale with s = powf(freq_base, -2/n_dims) (taken on the host, then applied by
+ * repeated float multiplication, as ggml's CPU backend does); dims from n_dims on are copied.
+ * -------------------------------------------------------------------------------------------- */
+#define CVATTN_ROPE_NORMAL 0
+#define CVATTN_ROPE_NEOX 2
+
+/* dst = rope(src): src/dst f32 [ne0, ne1, ne2, ne3] (any strides, nb0 = 4), pos i32 [ne2]
+ * (the position of each i2, as ggml_rope_ext takes it).  dst may alias src exactly. */
+CVATTN_API int cvattn_rope(const cvattn_tensor *dst, const cvattn_tensor *src, const cvattn_tensor *pos,
+                           int n_dims, int mode, float freq_base, float freq_scale, cvattn_stream_t stream);
+
+/* The KV write with RoPE fused in front: cvattn_set_rows(dst, rope(src), idx) without the
+ * intermediate tensor.  This is cosyvoice_kv_cache::update_cache (src/cosyvoice-kv-cache.cpp:
+ * 316,322) fed by the K rope of the same layer (src/cosyvoice-llm.cpp:57,
+ * src/cosyvoice-graph.cpp:352).  src is in the set_rows layout, f32 [ne0, n, ne2, ne3]; each row
+ * is ne0/head rope inputs of `head` elements (head 64 for the LLM's H_kv heads, 1024 for the DiT
+ * row that ggml_rope sees as one head).  pos is i32, contiguous, one position per source row:
+ * row (i1, i2, i3) takes pos[i1 + n*(i2 + ne2*i3)] -- the flattened position_ids the callers pass
+ * to both ops.  dst and idx follow cvattn_set_rows. */
+CVATTN_API int cvattn_rope_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src, const cvattn_tensor *idx,
+                                    const cvattn_tensor *pos, int64_t head, int n_dims, int mode, float freq_base,
+                                    float freq_scale, cvattn_stream_t stream);
+
 /* Human-readable name of a status code. */
 CVATTN_API const char *cvattn_status_string(int status);
 

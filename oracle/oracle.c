@@ -809,3 +809,41 @@ int or_set_rows(void *dst, int dst_type, size_t dst_nb1, int64_t dst_rows, const
     }
     return 0;
 }
+
+/* ggml_rope_ext (ggml-cpu/ops.cpp rope_f32 with rope_cache_init / rope_yarn; not vendored), for
+ * freq_factors NULL, ext_factor 0, attn_factor 1: the cache of (cos, sin) per pair is filled
+ * from theta = p, multiplied by theta_scale after each pair; rope_yarn then takes
+ * theta * freq_scale and cosf/sinf of it.  NORMAL rotates (x[2k], x[2k+1]); NEOX rotates
+ * (x[k], x[k + n_dims/2]).  Called at src/cosyvoice-llm.cpp:56-57 and
+ * src/cosyvoice-graph.cpp:351-352. */
+int or_rope_f32(const float *src, float *dst, int64_t ne0, int64_t n_rows, const int32_t *pos, int n_dims,
+                int mode, float freq_base, float freq_scale) {
+    if (n_dims <= 0 || (n_dims & 1) || n_dims > ne0 || (ne0 & 1)) return -1;
+    if (mode != OR_ROPE_NORMAL && mode != OR_ROPE_NEOX) return -1;
+    const float theta_scale = powf(freq_base, -2.0f / (float)n_dims);
+    float *cs = (float *)malloc(sizeof(float) * (size_t)n_dims);
+    if (!cs) return -1;
+    for (int64_t r = 0; r < n_rows; r++) {
+        const float *x = src + r * ne0;
+        float *y = dst + r * ne0;
+        float theta = (float)pos[r];
+        for (int i0 = 0; i0 < n_dims; i0 += 2) {
+            const float t = freq_scale * theta;
+            cs[i0] = cosf(t);
+            cs[i0 + 1] = sinf(t);
+            theta *= theta_scale;
+        }
+        const int half = n_dims / 2;
+        for (int i0 = 0; i0 < n_dims; i0 += 2) {
+            const int a = mode == OR_ROPE_NEOX ? i0 / 2 : i0;
+            const int b = mode == OR_ROPE_NEOX ? i0 / 2 + half : i0 + 1;
+            const float c = cs[i0], sn = cs[i0 + 1];
+            const float x0 = x[a], x1 = x[b];
+            y[a] = x0 * c - x1 * sn;
+            y[b] = x0 * sn + x1 * c;
+        }
+        for (int64_t i = n_dims; i < ne0; i++) y[i] = x[i];
+    }
+    free(cs);
+    return 0;
+}

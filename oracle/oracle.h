@@ -15,7 +15,9 @@
  *     src/cosyvoice-graph.cpp:375-376, as an fp64 textbook softmax(QK^T*scale+mask)V;
  *   - ggml's CPU flash-attention loop (ggml-cpu/ops.cpp), as the reported CPU baseline;
  *   - the caller-built masks (src/cosyvoice-llm.cpp:20-29, src/cosyvoice-token2wav.cpp:285-298);
- *   - the KV write ggml_set_rows (src/cosyvoice-kv-cache.cpp:316,322).
+ *   - the KV write ggml_set_rows (src/cosyvoice-kv-cache.cpp:316,322);
+ *   - the rotary embedding the callers apply to Q and K before it, ggml_rope_ext
+ *     (src/cosyvoice-llm.cpp:56-57, src/cosyvoice-graph.cpp:351-352).
  *
  * Pinning (how each function is checked beyond retyping it; see tests/test_oracle_*.py):
  *   or_fp32_to_fp16 / or_fp16_to_fp32 : exhaustive vs numpy float16 casts (all 65536 halves,
@@ -34,6 +36,13 @@
  *   or_causal_mask / or_chunk_mask    : brute-force predicate checks.
  *   or_set_rows                       : equals or_quantize_row per row (by construction) and
  *                                       is checked for untouched rows / index semantics.
+ *   or_rope_f32                       : position 0 is the identity; a hand-computed known answer
+ *                                       (x = (1, 0) at p = 1 gives (cos 1, sin 1)); float64
+ *                                       rotation by the same float32 angles; angles against the
+ *                                       closed form p * base^(-2k/n); pair norms preserved;
+ *                                       scores depend only on the position difference; NEOX is
+ *                                       NORMAL under the pairing permutation (bit-exact); dims
+ *                                       from n_dims on copied bit-exactly.
  */
 #ifndef CVATTN_ORACLE_H
 #define CVATTN_ORACLE_H
@@ -103,6 +112,17 @@ void or_chunk_mask(uint16_t *mask, int64_t n, const uint32_t *bounds, int64_t n_
  * with row stride dst_nb1; src f32 rows of ne0 with stride src_nb1. */
 int or_set_rows(void *dst, int dst_type, size_t dst_nb1, int64_t dst_rows, const float *src,
                 size_t src_nb1, int64_t ne0, const int32_t *idx, int64_t n_rows);
+
+/* ggml_rope_ext with freq_factors NULL, ext_factor 0 and attn_factor 1 (the forms cosyvoice.cpp
+ * calls: src/cosyvoice-llm.cpp:56-57 NEOX with theta from the GGUF; src/cosyvoice-graph.cpp:351-352
+ * ggml_rope NORMAL, base 10000, 64 rotated dims of a 1024-wide row).  n_rows contiguous f32 rows
+ * of ne0 elements; row r is at position pos[r].  Pair k (k < n_dims/2) is (2k, 2k+1) for NORMAL
+ * and (k, k + n_dims/2) for NEOX, rotated by theta_k = p * s^k with s = powf(freq_base,
+ * -2/n_dims) applied by repeated float multiplication, then times freq_scale; elements from
+ * n_dims on are copied. */
+enum { OR_ROPE_NORMAL = 0, OR_ROPE_NEOX = 2 };
+int or_rope_f32(const float *src, float *dst, int64_t ne0, int64_t n_rows, const int32_t *pos, int n_dims,
+                int mode, float freq_base, float freq_scale);
 
 #ifdef __cplusplus
 }

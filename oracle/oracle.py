@@ -14,6 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0 = 0, 1, 2, 3, 6, 7, 8
+ROPE_NORMAL, ROPE_NEOX = 0, 2
 BLOCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32}
 TYPE_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34}
 QUANT_TYPES = [Q8_0, Q4_0, Q4_1, Q5_0, Q5_1]
@@ -77,6 +78,8 @@ class Oracle:
         L.or_chunk_mask.argtypes = [vp, i64, vp, i64]
         L.or_set_rows.argtypes = [vp, ctypes.c_int, ctypes.c_size_t, i64, vp, ctypes.c_size_t, i64, vp, i64]
         L.or_set_rows.restype = ctypes.c_int
+        L.or_rope_f32.argtypes = [vp, vp, i64, i64, vp, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float]
+        L.or_rope_f32.restype = ctypes.c_int
         self.L = L
 
     # -- fp16 --
@@ -166,6 +169,19 @@ class Oracle:
         rc = self.L.or_set_rows(dst.ctypes.data, dst_type, dst_nb1, dst_rows, src.ctypes.data, src.shape[-1] * 4,
                                 src.shape[-1], idx.ctypes.data, idx.size)
         assert rc == 0
+
+    def rope(self, x: np.ndarray, pos, n_dims: int, mode: int, freq_base: float, freq_scale: float = 1.0) -> np.ndarray:
+        """ggml_rope_ext on rows of x[..., ne0]; pos gives one position per row (x.shape[:-1])."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        ne0 = x.shape[-1]
+        n_rows = x.size // ne0
+        p = np.ascontiguousarray(np.broadcast_to(np.asarray(pos, dtype=np.int32), x.shape[:-1])).reshape(-1)
+        y = np.empty_like(x)
+        rc = self.L.or_rope_f32(x.ctypes.data, y.ctypes.data, ne0, n_rows, p.ctypes.data, n_dims, mode,
+                                freq_base, freq_scale)
+        if rc:
+            raise ValueError("or_rope_f32 rejected its arguments")
+        return y
 
 
 _oracle = None

@@ -127,3 +127,29 @@ def test_set_rows_validation(eng):
 def test_library_is_loaded_from_tree(eng):
     assert os.path.dirname(eng.path) == os.path.join(ROOT, "cosyvoice.cpp_amd")
     assert isinstance(eng.L, ctypes.CDLL)
+
+
+def test_rope_argument_checks(eng):
+    """cvattn_rope / cvattn_rope_set_rows reject what ggml_rope_ext would not compute the same way;
+    every case returns before any kernel launch."""
+    x = cvattn.contiguous(FAKE, F32, [64, 14, 5, 1])
+    pos = cvattn.contiguous(FAKE, cvattn.I32, [5, 1, 1, 1])
+    assert eng.rope(x, x, pos, 64, 1, 1e6) == cvattn.ERR_UNSUPPORTED        # GLM/vision modes
+    assert eng.rope(x, x, pos, 63, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS  # odd dims
+    assert eng.rope(x, x, pos, 66, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS  # dims > ne0
+    assert eng.rope(x, x, pos, 64, cvattn.ROPE_NEOX, 0.0) == cvattn.ERR_BAD_ARGS  # base
+    pos4 = cvattn.contiguous(FAKE, cvattn.I32, [4, 1, 1, 1])
+    assert eng.rope(x, x, pos4, 64, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS  # one per i2
+    h16 = cvattn.contiguous(FAKE, F16, [64, 14, 5, 1])
+    assert eng.rope(h16, x, pos, 64, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_UNSUPPORTED
+
+    cache = cvattn.contiguous(FAKE, Q8_0, [128, 4096, 1, 1])
+    src = cvattn.contiguous(FAKE, F32, [128, 3, 1, 1])
+    idx = cvattn.contiguous(FAKE, cvattn.I32, [3, 1, 1, 1])
+    rs = eng.rope_set_rows
+    assert rs(cache, src, idx, idx, 96, 64, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS   # 128 % 96
+    assert rs(cache, src, idx, idx, 64, 80, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS   # dims > head
+    assert rs(cache, src, idx, idx, 64, 64, 8, 1e6) == cvattn.ERR_UNSUPPORTED
+    assert rs(cache, src, idx, pos4, 64, 64, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_BAD_ARGS  # 4 != 3 rows
+    posf = cvattn.contiguous(FAKE, F32, [3, 1, 1, 1])
+    assert rs(cache, src, idx, posf, 64, 64, cvattn.ROPE_NEOX, 1e6) == cvattn.ERR_UNSUPPORTED
