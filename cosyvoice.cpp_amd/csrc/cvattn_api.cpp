@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <limits>
 #include <vector>
 
 #include "cvattn_common.h"
@@ -56,17 +57,39 @@ struct FaShape {
     FaKernelShape ks;
 };
 
+// Transposed V of the non-flash-attention path: [n_kv, Dv, H_kv, B] of f32/f16 with the tokens
+// contiguous (src/cosyvoice-kv-cache.cpp:338-345: the view over the [max_seq, H_kv*Dv] cache).
+bool vt_ok(const cvattn_tensor *t) {
+    if (!t || !t->data || (t->type != T_F32 && t->type != T_F16)) return false;
+    if (t->ne[1] != HEAD || t->nb[0] != (size_t)type_bytes(t->type)) return false;
+    // element alignment (f32 rows are then 4-byte aligned; f16 rows may be 2-byte aligned)
+    if (((uintptr_t)t->data | (uintptr_t)t->nb[1] | (uintptr_t)t->nb[2] | (uintptr_t)t->nb[3]) % t->nb[0]) return false;
+    for (int i = 2; i < 4; i++)
+        if (t->ne[i] <= 0) return false;
+    if (t->ne[0] < 0) return false;
+    // the kernel addresses one head's [n_kv, Dv] with 32-bit byte offsets
+    return (int64_t)(HEAD - 1) * (int64_t)t->nb[1] + t->ne[0] * (int64_t)t->nb[0] < ((int64_t)1 << 31);
+}
+
+// vt: v is the transposed view of the non-flash-attention path (always the row-tiled kernel).
 int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
-             const cvattn_tensor *mask, FaShape *sh) {
+             const cvattn_tensor *mask, FaShape *sh, bool vt = false) {
     if (!q || !k || !v) return CVATTN_ERR_BAD_ARGS;
     if (!q->data) return CVATTN_ERR_BAD_ARGS;
     if (q->type != T_F32 && q->type != T_F16) return CVATTN_ERR_UNSUPPORTED;
-    if (q->ne[0] != HEAD || k->ne[0] != HEAD || v->ne[0] != HEAD) return CVATTN_ERR_UNSUPPORTED;
+    if (q->ne[0] != HEAD || k->ne[0] != HEAD || (vt ? v->ne[1] : v->ne[0]) != HEAD) return CVATTN_ERR_UNSUPPORTED;
     if (q->nb[0] != (size_t)type_bytes(q->type)) return CVATTN_ERR_UNSUPPORTED;
-    if (!kv_ok(k) || !kv_ok(v)) return is_kv_type(k->type) && is_kv_type(v->type) ? CVATTN_ERR_BAD_ARGS : CVATTN_ERR_UNSUPPORTED;
+    if (!kv_ok(k)) return is_kv_type(k->type) ? CVATTN_ERR_BAD_ARGS : CVATTN_ERR_UNSUPPORTED;
+    if (vt) {
+        // the non-flash-attention V cache must be f32/f16 (src/cosyvoice-loader.cpp:639-641)
+        if (v->type != T_F32 && v->type != T_F16) return CVATTN_ERR_UNSUPPORTED;
+        if (!vt_ok(v)) return CVATTN_ERR_BAD_ARGS;
+    } else if (!kv_ok(v)) {
+        return is_kv_type(v->type) ? CVATTN_ERR_BAD_ARGS : CVATTN_ERR_UNSUPPORTED;
+    }
     for (int i = 1; i < 4; i++)
         if (q->ne[i] <= 0) return CVATTN_ERR_BAD_ARGS;
-    if (k->ne[1] != v->ne[1]) return CVATTN_ERR_BAD_ARGS;
+    if (k->ne[1] != (vt ? v->ne[0] : v->ne[1])) return CVATTN_ERR_BAD_ARGS;
     if (k->ne[2] != v->ne[2]) return CVATTN_ERR_UNSUPPORTED;
     if (q->ne[2] % k->ne[2]) return CVATTN_ERR_BAD_ARGS;
     if (q->ne[3] % k->ne[3] || q->ne[3] % v->ne[3]) return CVATTN_ERR_BAD_ARGS;
@@ -88,8 +111,8 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     // 32-bit buffer offsets cover the K/V rows a decode workgroup reads (two heads when paired)
     const int64_t lim31 = ((int64_t)1 << 31) - 1;
     const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] + 2 * (int64_t)k->nb[2] < lim31 &&
-                       (int64_t)v->ne[1] * (int64_t)v->nb[1] + 2 * (int64_t)v->nb[2] < lim31;
-    sh->ks = fa_shape(sh->n_rows, sh->H_kv, small, mask && mask->data);
+                       (vt || (int64_t)v->ne[1] * (int64_t)v->nb[1] + 2 * (int64_t)v->nb[2] < lim31);
+    sh->ks = fa_shape(sh->n_rows, sh->H_kv, small && !vt, mask && mask->data);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
     sh->n_khg = sh->H_kv / sh->ks.hp;
     return CVATTN_OK;
@@ -186,6 +209,8 @@ void fill_problem(FaProblem &p, const cvattn_tensor *q, const cvattn_tensor *k, 
     p.n_kv = sh.n_kv;
     p.rk3 = (int32_t)(sh.B / k->ne[3]);
     p.rv3 = (int32_t)(sh.B / v->ne[3]);
+    // 16-byte loads need 4-byte aligned rows (a transposed f16 V over an odd max_seq has 2)
+    p.v_align2 = (((uintptr_t)v->data | (uintptr_t)v->nb[1] | (uintptr_t)v->nb[2] | (uintptr_t)v->nb[3]) & 3) != 0;
 }
 
 void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
@@ -221,8 +246,8 @@ struct SinglePlan {
 };
 
 int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
-                const cvattn_tensor *mask, SinglePlan *pl) {
-    int rc = check_fa(q, k, v, mask, &pl->sh);
+                const cvattn_tensor *mask, SinglePlan *pl, bool vt = false) {
+    int rc = check_fa(q, k, v, mask, &pl->sh, vt);
     if (rc) return rc;
     const FaShape &sh = pl->sh;
     plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len);
@@ -259,6 +284,10 @@ CVATTN_API size_t cvattn_flash_attn_ext_workspace(const cvattn_tensor *q, const 
     return pl.ws_bytes;
 }
 
+static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
+                      const cvattn_tensor *mask, const cvattn_tensor *dst, float scale, void *ws, size_t ws_bytes,
+                      cvattn_stream_t stream, bool vt);
+
 CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
                                      const cvattn_tensor *v, const cvattn_tensor *mask,
                                      const cvattn_tensor *dst, float scale, float max_bias,
@@ -267,8 +296,16 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
     if (max_bias != 0.0f || logit_softcap != 0.0f) return CVATTN_ERR_UNSUPPORTED;
     if (prec != CVATTN_PREC_DEFAULT && prec != CVATTN_PREC_F32) return CVATTN_ERR_BAD_ARGS;
     if (!std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
+    return run_single(q, k, v, mask, dst, scale, ws, ws_bytes, stream, false);
+}
+
+// One problem, one launch (plus the split merge).  vt: the non-flash-attention form (transposed
+// V, soft_max's NaN for a row with every key masked).
+static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
+                      const cvattn_tensor *mask, const cvattn_tensor *dst, float scale, void *ws, size_t ws_bytes,
+                      cvattn_stream_t stream, bool vt) {
     SinglePlan pl;
-    int rc = plan_single(q, k, v, mask, &pl);
+    int rc = plan_single(q, k, v, mask, &pl, vt);
     if (rc) return rc;
     rc = check_dst(dst, pl.sh);
     if (rc) return rc;
@@ -276,6 +313,7 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
     FaArgs a;
     std::memset(&a, 0, sizeof(a));
     fill_uniform(a.u, pl.sh, q->type, scale);
+    if (vt) a.u.empty_row = std::numeric_limits<float>::quiet_NaN();
     fill_problem(a.p0, q, k, v, mask, dst, pl.sh);
     a.p0.n_splits = pl.n_splits;
     a.p0.div_splits = make_fastdiv((uint32_t)pl.n_splits);
@@ -286,7 +324,32 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
     a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
     a.u.partials = (float *)ws;
     const bool has_mask = mask && mask->data;
+    if (vt)
+        return hip_status(fa_launch_vt(k->type, v->type == T_F32 ? T_VT_F32 : T_VT_F16, has_mask, a,
+                                       (hipStream_t)stream));
     return hip_status(fa_launch(pl.sh.ks, k->type, v->type, has_mask, false, a, (hipStream_t)stream));
+}
+
+// ---- the non-flash-attention node sequence ----------------------------------------------------
+
+CVATTN_API int cvattn_supports_attn_nonfa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *vt,
+                                          const cvattn_tensor *mask) {
+    FaShape sh;
+    return check_fa(q, k, vt, mask, &sh, true) == CVATTN_OK ? 1 : 0;
+}
+
+CVATTN_API size_t cvattn_attn_nonfa_workspace(const cvattn_tensor *q, const cvattn_tensor *k,
+                                              const cvattn_tensor *vt, const cvattn_tensor *mask) {
+    SinglePlan pl;
+    if (plan_single(q, k, vt, mask, &pl, true)) return 0;
+    return pl.ws_bytes;
+}
+
+CVATTN_API int cvattn_attn_nonfa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *vt,
+                                 const cvattn_tensor *mask, const cvattn_tensor *dst, float scale, void *ws,
+                                 size_t ws_bytes, cvattn_stream_t stream) {
+    if (!std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
+    return run_single(q, k, vt, mask, dst, scale, ws, ws_bytes, stream, true);
 }
 
 // ---- batches ------------------------------------------------------------------------------

@@ -46,6 +46,12 @@ __host__ __device__ constexpr int code_off(int t) {
 __host__ __device__ constexpr bool has_min(int t) { return t == T_Q4_1 || t == T_Q5_1; }
 __host__ __device__ constexpr bool is_quant(int t) { return type_block(t) == QK; }
 
+// V held transposed -- [n_kv, Dv] per head with the tokens contiguous, the V cache of the
+// non-flash-attention path (src/cosyvoice-kv-cache.cpp:104-108,338-345) -- in f32 or f16.
+// Kernel tags only, never ggml type codes.
+constexpr int T_VT_F32 = 64, T_VT_F16 = 65;
+__host__ __device__ constexpr bool is_vt(int t) { return t == T_VT_F32 || t == T_VT_F16; }
+
 // Division by a runtime constant d >= 1 for 0 <= n < 2^31: q = (n * mul) >> shift with
 // shift = 31 + ceil(log2 d) and mul = ceil(2^shift / d) < 2^32 (round-up method; the error term
 // n*(mul*d - 2^shift) / (d*2^shift) < 1/d never carries the quotient over).  Workgroup indices
@@ -80,6 +86,7 @@ struct FaProblem {
     int32_t n_splits;
     int32_t split_len;    // tokens per split (multiple of the kernel's token step)
     int32_t rk3, rv3;     // B / B_k, B / B_v
+    int32_t v_align2;     // transposed V whose rows are only 2-byte aligned (odd max_seq, f16)
     int64_t unit_begin;   // first workgroup unit of this problem in the launch
     int64_t part_begin;   // first partial slot (rows) of this problem in the workspace
     int64_t row_begin;    // first output row (b, i, h) of this problem (combine indexing)
@@ -96,6 +103,8 @@ struct FaUniform {
     int32_t n_problems;
     float scale;         // softmax scale
     float scale_log2;    // scale * log2(e)
+    float empty_row;     // output of a row whose keys are all masked: 0 (flash attention), or
+                         // NaN as ggml's soft_max gives it (the non-flash-attention path)
     int32_t n_khg;       // kv-head groups per batch entry (H_kv / kv heads per workgroup)
     FastDiv div_khg, div_rowgroups, div_upp; // n_khg, n_rowgroups, units_per_problem
     int64_t units_per_problem; // > 0 when every problem has this many workgroup units

@@ -20,6 +20,8 @@ struct FaKernelShape {
 FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
+// Row-tiled attention over a transposed V (vtype T_VT_F32 / T_VT_F16), single calls.
+hipError_t fa_launch_vt(int ktype, int vtype, bool mask, const FaArgs &a, hipStream_t st);
 
 hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st);
 

@@ -8,6 +8,7 @@ static FaLaunchFn fa_pick_decode(int mask, int batch, int hp, int ki, int vi) {
     return hp == 2 ? fa_pick_decode_m0_h2(batch, ki, vi) : fa_pick_decode_m0_h1(batch, ki, vi);
 }
 FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
+FaLaunchFn fa_pick_rows_vt(int mask, int ki, int vti);
 
 static int type_index(int t) {
     switch (t) {
@@ -43,6 +44,13 @@ hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bo
     if (ki < 0 || vi < 0) return hipErrorInvalidValue;
     const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, s.hp, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
     return fn(a, st);
+}
+
+hipError_t fa_launch_vt(int ktype, int vtype, bool mask, const FaArgs &a, hipStream_t st) {
+    const int ki = type_index(ktype);
+    const int vti = vtype == T_VT_F32 ? 0 : vtype == T_VT_F16 ? 1 : -1;
+    if (ki < 0 || vti < 0) return hipErrorInvalidValue;
+    return fa_pick_rows_vt(mask, ki, vti)(a, st);
 }
 
 } // namespace cvattn

@@ -193,22 +193,57 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     const int nsteps = (max(0, t_end - t_begin) + TS - 1) / TS; // uniform
 
     // ---- staging role: waves 0-1 stage K blocks, waves 2-3 V blocks; thread = (token, block) ----
+    // Transposed V (non-flash-attention layout): thread = (dim, 16-byte run of tokens), VNCH runs
+    // VDSTEP dims apart; the tile is kept dim-major in LDS, which is already the V^T operand.
+    constexpr bool VTR = is_vt(VT);
+    constexpr int VES = VT == T_VT_F32 ? 4 : 2;  // bytes per transposed-V element
+    constexpr int VCH = 16 / VES;                 // tokens per 16-byte run
+    constexpr int VCPD = TS / VCH;                // runs per dim of a tile
+    constexpr int VDSTEP = 128 / VCPD;            // dims between one thread's runs
+    constexpr int VNCH = HEAD / VDSTEP;           // runs per staging thread
     const bool stage_k = wv < 2; // uniform per wave
     const int st_tok = (tid & 127) >> 1, st_b = tid & 1;
+    const int vt_tc = (tid & 127) % VCPD, vt_d0 = (tid & 127) / VCPD;
     gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
     gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
     const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
-    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>() : 0;
+    // transposed f16: +2 bytes so the dword holding the last element is inside the range
+    // (buffer loads check whole dwords; the extra element is zeroed with the tile's tail)
+    const int64_t vext = P.n_kv <= 0 ? 0
+                         : VTR    ? (int64_t)(HEAD - 1) * P.v_nb1 + (int64_t)P.n_kv * VES + (VES == 2 ? 2 : 0)
+                                  : (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>();
     const __amdgpu_buffer_rsrc_t rsrc = stage_k ? make_rsrc(kbase, kext) : make_rsrc(vbase, vext);
-    const int nb1 = stage_k ? (int)P.k_nb1 : (int)P.v_nb1;
-    const int voff = st_tok * nb1 + st_b * (stage_k ? dblk_bytes<KT>() : dblk_bytes<VT>());
+    const int nb1 = stage_k ? (int)P.k_nb1 : VTR ? VES : (int)P.v_nb1; // bytes per token
+    const int voff = stage_k ? st_tok * nb1 + st_b * dblk_bytes<KT>()
+                     : VTR   ? vt_d0 * (int)P.v_nb1 + 16 * vt_tc
+                             : st_tok * nb1 + st_b * dblk_bytes<VT>();
 
     RawBuf<W> R0, R1;
     auto load_tile = [&](int t0, RawBuf<W> &r) {
-        if (stage_k)
+        if (stage_k) {
             blk_load<KT>(rsrc, voff, t0 * nb1, r);
-        else
+        } else if constexpr (VTR) {
+            if (P.v_align2) { // uniform: fp16 runs at 2-byte alignment, loaded element by element
+#pragma unroll
+                for (int i = 0; i < VNCH; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const int o = voff + i * VDSTEP * (int)P.v_nb1 + 4 * j;
+                        r.w[4 * i + j] = bld_u16(rsrc, o, t0 * VES) | (bld_u16(rsrc, o + 2, t0 * VES) << 16);
+                    }
+            } else {
+#pragma unroll
+                for (int i = 0; i < VNCH; i++) {
+                    const u4 a = bld_u128(rsrc, voff + i * VDSTEP * (int)P.v_nb1, t0 * VES);
+                    r.w[4 * i + 0] = a[0];
+                    r.w[4 * i + 1] = a[1];
+                    r.w[4 * i + 2] = a[2];
+                    r.w[4 * i + 3] = a[3];
+                }
+            }
+        } else {
             blk_load<VT>(rsrc, voff, t0 * nb1, r);
+        }
     };
     if (nsteps > 0) load_tile(t_begin, R0);
     if (nsteps > 1) load_tile(t_begin + TS, R1);
@@ -277,14 +312,36 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     }
     constexpr float kbias = stage_bias<KT>();
 
-    // unpack a staged tile's blocks into LDS buffer `buf`
-    auto write_tile = [&](const RawBuf<W> &r, int buf) {
+    // unpack a staged tile's blocks (tokens t0..t0+TS) into LDS buffer `buf`
+    auto write_tile = [&](const RawBuf<W> &r, int buf, int t0) {
         float d, m;
         if (stage_k) {
             blk_stage<KT, false>(r, sK[buf] + st_tok * RS + 32 * st_b);
             blk_scales<KT>(r, d, m);
             sS[buf][0][st_b][st_tok] = d * smul;
             if constexpr (has_min(KT)) sS[buf][1][st_b][st_tok] = m * smul;
+        } else if constexpr (VTR) {
+            // dim-major rows of fp16; tokens from n_kv on are zeroed (the cache row continues
+            // past them with whatever the cache holds, and they meet zero weights)
+            const int nvalid = P.n_kv - t0 - VCH * vt_tc; // valid tokens of each run
+#pragma unroll
+            for (int i = 0; i < VNCH; i++) {
+                _Float16 *dst = sV[buf] + (vt_d0 + VDSTEP * i) * RS + VCH * vt_tc;
+                if constexpr (VT == T_VT_F16) {
+                    u4 w = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
+                    if (t0 + TS > P.n_kv) { // uniform: the cache's last tile
+#pragma unroll
+                        for (int j = 0; j < 4; j++)
+                            w[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
+                    }
+                    *(u4 *)dst = w;
+                } else {
+                    h4 h;
+#pragma unroll
+                    for (int j = 0; j < 4; j++) h[j] = j < nvalid ? (_Float16)as_f32(r.w[4 * i + j]) : (_Float16)0.0f;
+                    *(h4 *)dst = h;
+                }
+            }
         } else {
             blk_stage<VT, true>(r, sV[buf] + st_tok * RS + 32 * st_b);
             blk_scales<VT>(r, d, m);
@@ -486,12 +543,20 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
             const int vrow = 32 * kb + 4 * g + (col >> 2);
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const _Float16 *va = cV + vrow * RS + 16 * i + 4 * (col & 3);
-                const h4 lo = __builtin_bit_cast(
-                    h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)va));
-                const h4 hi = __builtin_bit_cast(
-                    h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (__attribute__((address_space(3))) short4_t *)(va + 16 * RS)));
+                h4 lo, hi;
+                if constexpr (VTR) {
+                    // dim-major tile: dim 16i+col, tokens 4g..4g+3 and 16+4g..16+4g+3 of the 32
+                    const _Float16 *va = cV + (16 * i + col) * RS + 32 * kb + 4 * g;
+                    lo = *(const h4 *)va;
+                    hi = *(const h4 *)(va + 16);
+                } else {
+                    const _Float16 *va = cV + vrow * RS + 16 * i + 4 * (col & 3);
+                    lo = __builtin_bit_cast(
+                        h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)va));
+                    hi = __builtin_bit_cast(
+                        h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                (__attribute__((address_space(3))) short4_t *)(va + 16 * RS)));
+                }
                 const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
                 for (int r = 0; r < NR; r++)
@@ -503,7 +568,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     // ---- pipeline: tile s computes from LDS while tile s+1 is unpacked into the other buffer
     //      from registers loaded two steps earlier ----
     if (nsteps > 0) {
-        write_tile(R0, 0);
+        write_tile(R0, 0, t_begin);
         if (nsteps > 2) load_tile(t_begin + 2 * TS, R0);
     }
     __syncthreads();
@@ -514,7 +579,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         // even step: compute buffer 0, stage tile s0+1 (R1) into buffer 1
         compute_tile(0, t_begin + s0 * TS, std::true_type{});
         if (s0 + 1 < nsteps) {
-            write_tile(R1, 1);
+            write_tile(R1, 1, t_begin + (s0 + 1) * TS);
             if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TS, R1);
         }
         __syncthreads();
@@ -522,7 +587,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         // odd step: compute buffer 1, stage tile s0+2 (R0) into buffer 0
         compute_tile(1, t_begin + (s0 + 1) * TS, std::true_type{});
         if (s0 + 2 < nsteps) {
-            write_tile(R0, 0);
+            write_tile(R0, 0, t_begin + (s0 + 2) * TS);
             if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TS, R0);
         }
         __syncthreads();
@@ -543,7 +608,8 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         }
         if (row_ok[r]) {
             if (P.n_splits == 1) {
-                const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : 0.0f;
+                // a row with every key masked: 0 (flash attention) or NaN (soft_max path)
+                const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : U.empty_row;
                 float *o = P.dst + (((int64_t)bq * U.n_q + iq[r]) * U.H + hq[r]) * HEAD;
 #pragma unroll
                 for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[r][i] * inv;
@@ -627,7 +693,7 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
             acc += ps[d] * w;
         }
     }
-    P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d] = L > 0.0f ? acc / L : 0.0f;
+    P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d] = L > 0.0f ? acc / L : U.empty_row;
 }
 
 using FaLaunchFn = hipError_t (*)(const FaArgs &, hipStream_t);

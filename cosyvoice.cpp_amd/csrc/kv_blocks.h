@@ -28,7 +28,7 @@ __device__ __forceinline__ u4 bld_u128(__amdgpu_buffer_rsrc_t r, int v, int s) {
 
 template <int T>
 __host__ __device__ constexpr int blk_words() {
-    return T == T_F32 ? 32 : T == T_F16 ? 16 : T == T_Q8_0 ? 8 : 4;
+    return T == T_F32 || T == T_VT_F32 ? 32 : T == T_F16 || T == T_VT_F16 ? 16 : T == T_Q8_0 ? 8 : 4;
 }
 // bytes of 32 consecutive dims of a head row
 template <int T>

@@ -161,6 +161,12 @@ class Lib:
         L.cvattn_supports_set_rows.restype = ctypes.c_int
         L.cvattn_set_rows.argtypes = [P, P, P, vp]
         L.cvattn_set_rows.restype = ctypes.c_int
+        L.cvattn_supports_attn_nonfa.argtypes = [P, P, P, P]
+        L.cvattn_supports_attn_nonfa.restype = ctypes.c_int
+        L.cvattn_attn_nonfa_workspace.argtypes = [P, P, P, P]
+        L.cvattn_attn_nonfa_workspace.restype = sz
+        L.cvattn_attn_nonfa.argtypes = [P, P, P, P, P, ctypes.c_float, vp, sz, vp]
+        L.cvattn_attn_nonfa.restype = ctypes.c_int
         L.cvattn_rope.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, vp]
         L.cvattn_rope.restype = ctypes.c_int
         L.cvattn_rope_set_rows.argtypes = [P, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_float,
@@ -217,6 +223,16 @@ class Lib:
     def set_rows(self, dst, src, idx, stream=0) -> int:
         return int(self.L.cvattn_set_rows(self._p(dst), self._p(src), self._p(idx), stream or None))
 
+    def supports_attn_nonfa(self, q, k, vt, mask=None) -> bool:
+        return bool(self.L.cvattn_supports_attn_nonfa(self._p(q), self._p(k), self._p(vt), self._p(mask)))
+
+    def attn_nonfa_workspace(self, q, k, vt, mask=None) -> int:
+        return int(self.L.cvattn_attn_nonfa_workspace(self._p(q), self._p(k), self._p(vt), self._p(mask)))
+
+    def attn_nonfa(self, q, k, vt, mask, dst, scale, ws=0, ws_bytes=0, stream=0) -> int:
+        return int(self.L.cvattn_attn_nonfa(self._p(q), self._p(k), self._p(vt), self._p(mask), self._p(dst), scale,
+                                            ws or None, ws_bytes, stream or None))
+
     def rope(self, dst, src, pos, n_dims, mode, freq_base, freq_scale=1.0, stream=0) -> int:
         return int(self.L.cvattn_rope(self._p(dst), self._p(src), self._p(pos), n_dims, mode, freq_base, freq_scale,
                                       stream or None))
@@ -233,7 +249,8 @@ EXPORTED = [
     "cvattn_supports_flash_attn_ext", "cvattn_flash_attn_ext_workspace", "cvattn_flash_attn_ext",
     "cvattn_fa_batch_workspace", "cvattn_fa_batch_prepare", "cvattn_fa_batch_launch",
     "cvattn_block_size", "cvattn_type_size", "cvattn_dequantize",
-    "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_rope", "cvattn_rope_set_rows", "cvattn_status_string",
+    "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_rope", "cvattn_rope_set_rows",
+    "cvattn_supports_attn_nonfa", "cvattn_attn_nonfa_workspace", "cvattn_attn_nonfa", "cvattn_status_string",
 ]
 
 _lib = None

@@ -134,6 +134,26 @@ CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n,
 CVATTN_API int cvattn_fa_batch_launch(const cvattn_fa_plan *plan, cvattn_stream_t stream);
 
 /* --------------------------------------------------------------------------------------------
+ * The non-flash-attention path (--llm-flash-attn 0 / --flow-flash-attn 0): the node sequence
+ *   scores = mul_mat(K, Q) (prec F32) -> soft_max_ext(scores, mask, scale, 0)
+ *   -> mul_mat(V^T, weights) -> permute(0, 2, 1, 3) -> cont
+ * of src/cosyvoice-kv-cache.cpp:387-395 and src/cosyvoice-graph.cpp:378-388, in one call that
+ * never materialises the scores.  V is the transposed cache view that path keeps:
+ *   vt   f32/f16 [n_kv, Dv, H_kv, B_v], tokens contiguous (nb0 = element size), nb1 = the dim
+ *        stride (src/cosyvoice-kv-cache.cpp:345: view_4d(v, cur_len + n, Dv, heads, batch))
+ * q, k, mask, dst, scale and the workspace are as for cvattn_flash_attn_ext (K may be any KV
+ * type; the loader keeps V unquantized in this mode, src/cosyvoice-loader.cpp:639-641).  A row
+ * whose keys are all masked yields NaN, as ggml's soft_max does.
+ * -------------------------------------------------------------------------------------------- */
+CVATTN_API int cvattn_supports_attn_nonfa(const cvattn_tensor *q, const cvattn_tensor *k,
+                                          const cvattn_tensor *vt, const cvattn_tensor *mask);
+CVATTN_API size_t cvattn_attn_nonfa_workspace(const cvattn_tensor *q, const cvattn_tensor *k,
+                                              const cvattn_tensor *vt, const cvattn_tensor *mask);
+CVATTN_API int cvattn_attn_nonfa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *vt,
+                                 const cvattn_tensor *mask, const cvattn_tensor *dst, float scale, void *ws,
+                                 size_t ws_bytes, cvattn_stream_t stream);
+
+/* --------------------------------------------------------------------------------------------
  * Block formats.
  * -------------------------------------------------------------------------------------------- */
 
@@ -152,7 +172,9 @@ CVATTN_API int cvattn_dequantize(int type, const void *src, float *dst, int64_t 
  *   dst  cache tensor of a KV type, [ne0, rows, ne2, ne3]
  *   src  f32 [ne0, n, ne2, ne3]
  *   idx  i32 [n] (positions; ggml broadcasts a 1-D index over ne2/ne3)
- * Quantization follows ggml's quantize_row_*_ref bit for bit.
+ * Quantization follows ggml's quantize_row_*_ref bit for bit.  With ne0 = 1 it is the element
+ * scatter of the transposed V cache: dst/src flattened to [1, N] and idx the v_idxs the host
+ * fills (src/cosyvoice-kv-cache.cpp:338-343,357-377).
  * -------------------------------------------------------------------------------------------- */
 CVATTN_API int cvattn_supports_set_rows(const cvattn_tensor *dst, const cvattn_tensor *src,
                                         const cvattn_tensor *idx);

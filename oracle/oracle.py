@@ -184,6 +184,19 @@ class Oracle:
         return y
 
 
+def v_idxs(positions, n_tokens: int, n_tokens_per_batch: int, n_embd: int, max_seq: int) -> np.ndarray:
+    """The element-scatter index of the transposed V cache, as cosyvoice_kv_cache::set_input_v_idxs
+    fills it (src/cosyvoice-kv-cache.cpp:357-377): source element (token i, feature j) of the
+    flattened [n_embd, n_tokens] V goes to element base(i) + j*max_seq of the flattened
+    [max_seq, n_embd, batch] cache, base(i) = (i / n_tokens_per_batch)*max_seq*n_embd +
+    positions[i % n_tokens_per_batch]."""
+    pos = np.asarray(positions, dtype=np.int64)
+    i = np.arange(n_tokens, dtype=np.int64)
+    base = (i // n_tokens_per_batch) * max_seq * n_embd + pos[i % n_tokens_per_batch]
+    j = np.arange(n_embd, dtype=np.int64)
+    return (base[:, None] + j[None, :] * max_seq).reshape(-1).astype(np.int32)
+
+
 _oracle = None
 
 

@@ -177,3 +177,22 @@ def test_set_rows_oracle(orc, rng, t):
         assert np.array_equal(dst[i], orc.quantize(t, src[r]))
     untouched = [r for r in range(rows) if r not in idx]
     assert np.array_equal(dst[untouched], before[untouched])
+
+
+def test_v_idxs_is_the_transposed_write():
+    """Scattering V's elements through v_idxs (src/cosyvoice-kv-cache.cpp:338-343,357-377) equals
+    writing each token's features down the token column of the [max_seq, n_embd, batch] cache."""
+    from oracle.oracle import v_idxs
+    rng = np.random.default_rng(3)
+    for n_embd, max_seq, T, B in ((128, 40, 7, 1), (1024, 30, 5, 2), (8, 9, 9, 3)):
+        pos = rng.permutation(max_seq)[:T]
+        v = rng.standard_normal((B * T, n_embd)).astype(np.float32)   # token-major source rows
+        flat = np.zeros(B * n_embd * max_seq, np.float32)
+        flat[v_idxs(pos, B * T, T, n_embd, max_seq)] = v.reshape(-1)
+        cache = flat.reshape(B, n_embd, max_seq)                      # [batch][feature][token]
+        want = np.zeros_like(cache)
+        for b in range(B):
+            want[b][:, pos] = v[b * T:(b + 1) * T].T
+        assert np.array_equal(cache, want)
+        # every target distinct (no two elements collide)
+        assert len(np.unique(v_idxs(pos, B * T, T, n_embd, max_seq))) == B * T * n_embd
