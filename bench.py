@@ -315,8 +315,9 @@ def main():
                     help="only run 256 MiB device copies (reference kernels for the HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (this attention path has "
-              "no multi-GPU form here: see DESIGN.md for how it would shard)", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path runs "
+              "on one GPU: sequences, layers and DiT heads are independent work, so a multi-GPU form would "
+              "shard them with no exchange inside attention)", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -61,4 +61,17 @@ struct RopeArgs {
 };
 hipError_t rope_launch(const RopeArgs &a, hipStream_t st);
 
+// DiT step inputs built on the device.
+constexpr int kMaxChunkBounds = 256;
+struct ChunkMaskArgs {
+    uint8_t *mask;    // f16 rows of n_cols, nb1 bytes apart
+    int64_t nb1;
+    int32_t n_rows, n_cols, n_bounds;
+    uint32_t bounds[kMaxChunkBounds];
+};
+hipError_t chunk_mask_launch(const ChunkMaskArgs &a, hipStream_t st);
+hipError_t fill_positions_launch(int32_t *pos, int64_t n, int64_t batch, int64_t nb1, int32_t base, hipStream_t st);
+hipError_t v_idxs_launch(int32_t *idx, const int32_t *pos, uint32_t n_tokens, uint32_t n_per_batch, uint32_t n_embd,
+                         uint32_t max_seq, hipStream_t st);
+
 } // namespace cvattn

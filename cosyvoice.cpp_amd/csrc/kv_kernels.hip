@@ -283,8 +283,67 @@ __global__ __launch_bounds__(256) void set_rows_kernel(SetRowsArgs a) {
 }
 
 // ------------------------------------------------------------------------------------------
+// DiT step inputs (src/cosyvoice-token2wav.cpp:273-302, src/cosyvoice-kv-cache.cpp:357-377).
+// ------------------------------------------------------------------------------------------
+// One workgroup per mask row: the row's block end is the first chunk boundary above it (the
+// bounds are sorted; every thread scans them from the kernel arguments), then the row is filled
+// with 0 before it and fp16 -inf from it on.
+__global__ __launch_bounds__(256) void chunk_mask_kernel(ChunkMaskArgs a) {
+    const int i = blockIdx.x;
+    int end = a.n_cols;
+    for (int b = 0; b < a.n_bounds; b++)
+        if (a.bounds[b] > (uint32_t)i) {
+            end = (int)min((uint32_t)a.n_cols, a.bounds[b]);
+            break;
+        }
+    uint16_t *row = (uint16_t *)(a.mask + (int64_t)i * a.nb1);
+    for (int j = threadIdx.x; j < a.n_cols; j += blockDim.x) row[j] = j < end ? (uint16_t)0 : (uint16_t)0xFC00;
+}
+
+__global__ __launch_bounds__(256) void fill_positions_kernel(int32_t *pos, int64_t n, int64_t total, int64_t nb1,
+                                                            int32_t base) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const int64_t j = gid % n, b = gid / n;
+    *(int32_t *)((uint8_t *)pos + b * nb1 + 4 * j) = (int32_t)j + base;
+}
+
+// idx[i * n_embd + j] = (i / n_per_batch) * max_seq * n_embd + pos[i % n_per_batch] + j * max_seq,
+// in 32-bit arithmetic as the host loop forms it.
+__global__ __launch_bounds__(256) void v_idxs_kernel(int32_t *idx, const int32_t *pos, uint32_t n_tokens,
+                                                    uint32_t n_per_batch, uint32_t n_embd, uint32_t max_seq) {
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (int64_t)n_tokens * n_embd) return;
+    const uint32_t i = (uint32_t)(gid / n_embd), j = (uint32_t)(gid % n_embd);
+    const int32_t base = (int32_t)((i / n_per_batch) * max_seq * n_embd) + pos[i % n_per_batch];
+    idx[gid] = base + (int32_t)(j * max_seq);
+}
+
+// ------------------------------------------------------------------------------------------
 // Host launchers.
 // ------------------------------------------------------------------------------------------
+hipError_t chunk_mask_launch(const ChunkMaskArgs &a, hipStream_t st) {
+    if (a.n_rows <= 0 || a.n_cols <= 0) return hipSuccess;
+    hipLaunchKernelGGL(chunk_mask_kernel, dim3((unsigned)a.n_rows), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
+hipError_t fill_positions_launch(int32_t *pos, int64_t n, int64_t batch, int64_t nb1, int32_t base, hipStream_t st) {
+    const int64_t total = n * batch;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fill_positions_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, pos, n, total,
+                       nb1, base);
+    return hipGetLastError();
+}
+
+hipError_t v_idxs_launch(int32_t *idx, const int32_t *pos, uint32_t n_tokens, uint32_t n_per_batch, uint32_t n_embd,
+                         uint32_t max_seq, hipStream_t st) {
+    const int64_t total = (int64_t)n_tokens * n_embd;
+    if (total <= 0) return hipSuccess;
+    hipLaunchKernelGGL(v_idxs_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, idx, pos, n_tokens,
+                       n_per_batch, n_embd, max_seq);
+    return hipGetLastError();
+}
 hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (type == T_F32) {

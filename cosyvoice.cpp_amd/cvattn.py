@@ -57,6 +57,18 @@ class FaProblem(ctypes.Structure):
     _fields_ = [("q", Tensor), ("k", Tensor), ("v", Tensor), ("mask", Tensor), ("dst", Tensor)]
 
 
+class DitCacheParams(ctypes.Structure):
+    """cvattn_dit_cache_params"""
+    _fields_ = [(n, ctypes.c_int32) for n in ("layers", "heads", "head_dim", "max_seq", "batch", "k_type", "v_type",
+                                              "n_slots", "n_host_slots", "flash_attn")]
+
+
+class DitStep(ctypes.Structure):
+    """cvattn_dit_step"""
+    _fields_ = [(n, ctypes.c_int32) for n in ("rebuild", "cache_kv", "load", "offload", "slide", "slice", "mask",
+                                              "slot", "host_slot")] + [("cut_len", ctypes.c_int64)]
+
+
 class FaPlan(ctypes.Structure):
     _fields_ = [("opaque", ctypes.c_uint64 * 64)]
 
@@ -167,6 +179,40 @@ class Lib:
         L.cvattn_attn_nonfa_workspace.restype = sz
         L.cvattn_attn_nonfa.argtypes = [P, P, P, P, P, ctypes.c_float, vp, sz, vp]
         L.cvattn_attn_nonfa.restype = ctypes.c_int
+        DP = ctypes.POINTER(DitCacheParams)
+        L.cvattn_dit_cache_device_bytes.argtypes = [DP]
+        L.cvattn_dit_cache_device_bytes.restype = sz
+        L.cvattn_dit_cache_host_bytes.argtypes = [DP]
+        L.cvattn_dit_cache_host_bytes.restype = sz
+        L.cvattn_dit_cache_create.argtypes = [DP, vp, sz, vp, sz, ctypes.POINTER(vp)]
+        L.cvattn_dit_cache_create.restype = ctypes.c_int
+        L.cvattn_dit_cache_destroy.argtypes = [vp]
+        L.cvattn_dit_cache_destroy.restype = None
+        L.cvattn_dit_cache_bind_slot.argtypes = [vp, ctypes.c_int]
+        L.cvattn_dit_cache_bind_slot.restype = ctypes.c_int
+        L.cvattn_dit_cache_slide.argtypes = [vp]
+        L.cvattn_dit_cache_slide.restype = ctypes.c_int
+        L.cvattn_dit_cache_slot.argtypes = [vp]
+        L.cvattn_dit_cache_slot.restype = ctypes.c_int
+        L.cvattn_dit_cache_set_len.argtypes = [vp, ctypes.c_uint32]
+        L.cvattn_dit_cache_set_len.restype = ctypes.c_int
+        L.cvattn_dit_cache_len.argtypes = [vp]
+        L.cvattn_dit_cache_len.restype = ctypes.c_uint32
+        L.cvattn_dit_cache_layer.argtypes = [vp, ctypes.c_int, ctypes.c_int64, P, P, P, P]
+        L.cvattn_dit_cache_layer.restype = ctypes.c_int
+        L.cvattn_dit_cache_offload.argtypes = [vp, ctypes.c_int, ctypes.c_uint32, vp]
+        L.cvattn_dit_cache_offload.restype = ctypes.c_int
+        L.cvattn_dit_cache_load.argtypes = [vp, ctypes.c_int, vp]
+        L.cvattn_dit_cache_load.restype = ctypes.c_int
+        L.cvattn_fill_positions.argtypes = [P, ctypes.c_int32, vp]
+        L.cvattn_fill_positions.restype = ctypes.c_int
+        L.cvattn_chunk_mask.argtypes = [P, ctypes.POINTER(ctypes.c_uint32), ctypes.c_int, vp]
+        L.cvattn_chunk_mask.restype = ctypes.c_int
+        L.cvattn_v_idxs.argtypes = [vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, vp]
+        L.cvattn_v_idxs.restype = ctypes.c_int
+        L.cvattn_dit_schedule.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_uint32,
+                                          ctypes.c_int, ctypes.c_int, ctypes.POINTER(DitStep)]
+        L.cvattn_dit_schedule.restype = ctypes.c_int
         L.cvattn_rope.argtypes = [P, P, P, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_float, vp]
         L.cvattn_rope.restype = ctypes.c_int
         L.cvattn_rope_set_rows.argtypes = [P, P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, ctypes.c_float,
@@ -241,6 +287,39 @@ class Lib:
         return int(self.L.cvattn_rope_set_rows(self._p(dst), self._p(src), self._p(idx), self._p(pos), head, n_dims,
                                                mode, freq_base, freq_scale, stream or None))
 
+    # -- DiT streaming cache --
+    def dit_cache_bytes(self, params: DitCacheParams):
+        return (int(self.L.cvattn_dit_cache_device_bytes(ctypes.byref(params))),
+                int(self.L.cvattn_dit_cache_host_bytes(ctypes.byref(params))))
+
+    def dit_cache_create(self, params: DitCacheParams, dev_ptr, dev_bytes, host_ptr=0, host_bytes=0):
+        h = ctypes.c_void_p()
+        rc = self.L.cvattn_dit_cache_create(ctypes.byref(params), dev_ptr or None, dev_bytes, host_ptr or None,
+                                            host_bytes, ctypes.byref(h))
+        return rc, h
+
+    def dit_cache_layer(self, cache, layer, n_kv):
+        ts = [Tensor() for _ in range(4)]
+        rc = self.L.cvattn_dit_cache_layer(cache, layer, n_kv, *[ctypes.byref(t) for t in ts])
+        return rc, ts
+
+    def chunk_mask(self, mask, bounds, stream=0) -> int:
+        arr = (ctypes.c_uint32 * max(1, len(bounds)))(*[int(b) for b in bounds])
+        return int(self.L.cvattn_chunk_mask(self._p(mask), arr, len(bounds), stream or None))
+
+    def fill_positions(self, pos, base, stream=0) -> int:
+        return int(self.L.cvattn_fill_positions(self._p(pos), base, stream or None))
+
+    def v_idxs(self, idx_ptr, pos_ptr, n_tokens, n_per_batch, n_embd, max_seq, stream=0) -> int:
+        return int(self.L.cvattn_v_idxs(idx_ptr or None, pos_ptr or None, n_tokens, n_per_batch, n_embd, max_seq,
+                                        stream or None))
+
+    def dit_schedule(self, n_steps, n_fixed, n_offloadable, cut_len, offset, streaming, kv_slidable):
+        out = (DitStep * n_steps)()
+        rc = self.L.cvattn_dit_schedule(n_steps, n_fixed, n_offloadable, cut_len, offset, int(streaming),
+                                        int(kv_slidable), out)
+        return rc, list(out)
+
     def status_string(self, rc) -> str:
         return self.L.cvattn_status_string(rc).decode()
 
@@ -250,7 +329,11 @@ EXPORTED = [
     "cvattn_fa_batch_workspace", "cvattn_fa_batch_prepare", "cvattn_fa_batch_launch",
     "cvattn_block_size", "cvattn_type_size", "cvattn_dequantize",
     "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_rope", "cvattn_rope_set_rows",
-    "cvattn_supports_attn_nonfa", "cvattn_attn_nonfa_workspace", "cvattn_attn_nonfa", "cvattn_status_string",
+    "cvattn_supports_attn_nonfa", "cvattn_attn_nonfa_workspace", "cvattn_attn_nonfa",
+    "cvattn_dit_cache_device_bytes", "cvattn_dit_cache_host_bytes", "cvattn_dit_cache_create",
+    "cvattn_dit_cache_destroy", "cvattn_dit_cache_bind_slot", "cvattn_dit_cache_slide", "cvattn_dit_cache_slot",
+    "cvattn_dit_cache_set_len", "cvattn_dit_cache_len", "cvattn_dit_cache_layer", "cvattn_dit_cache_offload",
+    "cvattn_dit_cache_load", "cvattn_fill_positions", "cvattn_chunk_mask", "cvattn_v_idxs", "cvattn_dit_schedule", "cvattn_status_string",
 ]
 
 _lib = None

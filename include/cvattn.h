@@ -212,6 +212,97 @@ CVATTN_API int cvattn_rope_set_rows(const cvattn_tensor *dst, const cvattn_tenso
                                     const cvattn_tensor *pos, int64_t head, int n_dims, int mode, float freq_base,
                                     float freq_scale, cvattn_stream_t stream);
 
+/* --------------------------------------------------------------------------------------------
+ * DiT streaming KV cache (cosyvoice_kv_cache as the flow decoder uses it,
+ * src/cosyvoice-kv-cache.cpp:45-146,148-290,398-467, built at src/cosyvoice-loader.cpp:1011-1029;
+ * driven by the slot schedule of src/cosyvoice-token2wav.cpp:101-167,265-420).
+ *
+ * Slots: each cached ODE step keeps its own K/V (the DiT input differs per step).  n_slots
+ * device slots hold layers x {K, V} of [H*D, max_seq, batch] (V transposed to
+ * [max_seq, H*D, batch] when flash_attn is 0), slot-major, each tensor 256-byte aligned; slot 0
+ * is the staging slot of the offloadable steps, whose K/V rows move to pinned host slots between
+ * uses.  The caller allocates both buffers (sizes from the *_bytes calls) and keeps them for the
+ * cache's lifetime; the cache object itself only records layout and state.
+ * -------------------------------------------------------------------------------------------- */
+typedef struct cvattn_dit_cache cvattn_dit_cache;
+
+typedef struct cvattn_dit_cache_params {
+    int32_t layers;          /* DiT transformer blocks (22) */
+    int32_t heads;           /* attention heads = kv heads (16) */
+    int32_t head_dim;        /* 64 */
+    int32_t max_seq;         /* dit_kv_cache_length */
+    int32_t batch;           /* 2: the CFG pair */
+    int32_t k_type, v_type;  /* ggml type codes of the cache */
+    int32_t n_slots;         /* device slots: fixed slots + (offloadable slots ? 1 : 0) */
+    int32_t n_host_slots;    /* offloadable slots (host copies) */
+    int32_t flash_attn;      /* 1: V rows like K; 0: V transposed (non-flash-attention path) */
+} cvattn_dit_cache_params;
+
+CVATTN_API size_t cvattn_dit_cache_device_bytes(const cvattn_dit_cache_params *p);
+CVATTN_API size_t cvattn_dit_cache_host_bytes(const cvattn_dit_cache_params *p);
+/* Creates the cache over device_buf (device memory) and host_buf (pinned host memory, may be
+ * NULL when n_host_slots is 0).  Slot 0 is bound and the cached length is 0. */
+CVATTN_API int cvattn_dit_cache_create(const cvattn_dit_cache_params *p, void *device_buf, size_t device_bytes,
+                                       void *host_buf, size_t host_bytes, cvattn_dit_cache **out);
+CVATTN_API void cvattn_dit_cache_destroy(cvattn_dit_cache *c);
+
+/* bind_slot (kv-cache.cpp:415-420), slide_kv_slot (:422-465: the next slot takes over the
+ * views; flash attention only), and the cached length cur_len. */
+CVATTN_API int cvattn_dit_cache_bind_slot(cvattn_dit_cache *c, int slot);
+CVATTN_API int cvattn_dit_cache_slide(cvattn_dit_cache *c);
+CVATTN_API int cvattn_dit_cache_slot(const cvattn_dit_cache *c);
+CVATTN_API int cvattn_dit_cache_set_len(cvattn_dit_cache *c, uint32_t cur_len);
+CVATTN_API uint32_t cvattn_dit_cache_len(const cvattn_dit_cache *c);
+
+/* The bound slot's tensors of one layer, as update_cache uses them (kv-cache.cpp:309-355):
+ *   k_cache, v_cache  the whole cache tensors (set_rows targets; with flash_attn 0, v_cache is
+ *                     the transposed tensor [max_seq, H*D, batch] -- flatten it to [1, N] for
+ *                     the v_idxs scatter);
+ *   k_view, v_view    the attention views over n_kv = cur_len + n_new tokens: [D, n_kv, H, B]
+ *                     for K (and V with flash attention), [n_kv, D, H, B] for the transposed V.
+ * Any output pointer may be NULL. */
+CVATTN_API int cvattn_dit_cache_layer(const cvattn_dit_cache *c, int layer, int64_t n_kv, cvattn_tensor *k_cache,
+                                      cvattn_tensor *v_cache, cvattn_tensor *k_view, cvattn_tensor *v_view);
+
+/* offload_slot / load_slot (kv-cache.cpp:148-246,276-290): asynchronous copies of the first
+ * n_tokens rows of every layer's K and V of the bound slot to host slot `host_slot`, and back
+ * (load sets cur_len to the stored length).  The host layout per slot is layer-major,
+ * {K of batch 0..B-1, V of batch 0..B-1} of n_tokens rows each (the transposed V as its
+ * [n_tokens, H*D] block per batch).  Ordered on `stream`; the host data is complete after it. */
+CVATTN_API int cvattn_dit_cache_offload(cvattn_dit_cache *c, int host_slot, uint32_t n_tokens,
+                                        cvattn_stream_t stream);
+CVATTN_API int cvattn_dit_cache_load(cvattn_dit_cache *c, int host_slot, cvattn_stream_t stream);
+
+/* The DiT step inputs the host fills before each graph compute (token2wav.cpp:273-302), built
+ * on the device:
+ *   cvattn_fill_positions  pos i32 [n, B] contiguous: pos[b][j] = j + base (base = cur_len for
+ *                          cached steps, 0 otherwise);
+ *   cvattn_chunk_mask      f16 mask [n_cols, n_rows]: row i sees keys j < the first chunk
+ *                          boundary greater than i (n_cols if none), -inf beyond; bounds sorted
+ *                          ascending, at most CVATTN_MAX_CHUNK_BOUNDS of them;
+ *   cvattn_v_idxs          the element-scatter index of the transposed V write, as
+ *                          set_input_v_idxs builds it (kv-cache.cpp:357-377), from the device
+ *                          positions pos[0..n_per_batch): idx i32 [n_embd * n_tokens]. */
+#define CVATTN_MAX_CHUNK_BOUNDS 256
+CVATTN_API int cvattn_fill_positions(const cvattn_tensor *pos, int32_t base, cvattn_stream_t stream);
+CVATTN_API int cvattn_chunk_mask(const cvattn_tensor *mask, const uint32_t *bounds, int n_bounds,
+                                 cvattn_stream_t stream);
+CVATTN_API int cvattn_v_idxs(int32_t *idx, const int32_t *pos, uint32_t n_tokens, uint32_t n_per_batch,
+                             uint32_t n_embd, uint32_t max_seq, cvattn_stream_t stream);
+
+/* The per-ODE-step plan of a streaming (or one-shot) token2wav call, dit_sched_config
+ * (token2wav.cpp:101-167), with the device slot each step computes on and the host slot it loads
+ * or offloads (the bind/slide and offload counters of token2wav.cpp:352-412 replayed):
+ *   slot       device slot bound while the step runs (-1: no cache)
+ *   host_slot  host slot loaded before / offloaded after the step (-1: none) */
+typedef struct cvattn_dit_step {
+    int32_t rebuild, cache_kv, load, offload, slide, slice, mask;
+    int32_t slot, host_slot;
+    int64_t cut_len;
+} cvattn_dit_step;
+CVATTN_API int cvattn_dit_schedule(int n_steps, int n_fixed_slots, int n_offloadable_slots, int64_t cut_len,
+                                   uint32_t offset, int streaming, int kv_slidable, cvattn_dit_step *out);
+
 /* Human-readable name of a status code. */
 CVATTN_API const char *cvattn_status_string(int status);
 
