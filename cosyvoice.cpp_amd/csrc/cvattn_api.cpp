@@ -112,9 +112,9 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     const int64_t lim31 = ((int64_t)1 << 31) - 1;
     const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] + 2 * (int64_t)k->nb[2] < lim31 &&
                        (vt || (int64_t)v->ne[1] * (int64_t)v->nb[1] + 2 * (int64_t)v->nb[2] < lim31);
-    sh->ks = fa_shape(sh->n_rows, sh->H_kv, small && !vt, mask && mask->data);
+    sh->ks = fa_shape(sh->n_rows, small && !vt);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
-    sh->n_khg = sh->H_kv / sh->ks.hp;
+    sh->n_khg = sh->H_kv;
     return CVATTN_OK;
 }
 
@@ -132,18 +132,23 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 }
 
 // Token splits.  Decode-shaped problems (waves split the tokens) size each wave's token run so
-// the whole launch has ~kTargetWaves waves in flight; row-tiled problems split only when their
-// row groups alone cannot fill the chip.  `work` is the launch-wide sum of
-// B*n_khg*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
-constexpr int64_t kTargetWaves = 2048;
-constexpr int64_t kSmallDecodeWork = 4 * 8192; // kv-head-group tokens of a latency-bound launch
+// the whole launch has about kTargetWaves waves in flight (half that when each kv head has
+// several row groups, which already multiply the workgroups reading a head); row-tiled problems
+// split only when their row groups alone cannot fill the chip.  `work` is the launch-wide sum
+// of B*n_khg*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
+constexpr int64_t kTargetWaves = 4096;
+// Most token splits of a decode-shaped group: the last-arriving workgroup loads every split's
+// partial from one CU, and past 16 splits that merge costs more than the streaming it shortens
+// (24-layer 4096-token q8_0/q4_0 step and the one-layer launch both measured best at 16).
+constexpr int kDecodeMaxSplits = 16;
 
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
     const int tstep = sh.ks.tstep;
     int len;
     if (sh.ks.wsplit) {
-        // tokens per wave: a multiple of the wave step (tstep tokens of hp kv heads)
-        int64_t wlen = (std::max<int64_t>(1, work) + kTargetWaves - 1) / kTargetWaves;
+        // tokens per wave: a multiple of the wave step
+        const int64_t tw = sh.n_rowgroups > 1 ? kTargetWaves / 2 : kTargetWaves;
+        int64_t wlen = (std::max<int64_t>(1, work) + tw - 1) / tw;
         wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
         len = (int)wlen * sh.ks.nw;
     } else {
@@ -163,11 +168,8 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
     }
     const int unit = sh.ks.wsplit ? tstep * sh.ks.nw : tstep;
-    // Never more splits than the in-kernel merge takes in one pass.  The merging workgroup's
-    // loads are issued by one CU, so launches with enough work elsewhere (a few kv-head groups
-    // of long context or more) stop at half of that.
-    int max_splits = sh.ks.max_splits;
-    if (sh.ks.wsplit && work > kSmallDecodeWork) max_splits = std::max(1, max_splits / 2);
+    // never more splits than the in-kernel merge takes in one pass
+    const int max_splits = sh.ks.wsplit ? std::min(sh.ks.max_splits, kDecodeMaxSplits) : sh.ks.max_splits;
     const int min_len = (n_kv + max_splits - 1) / max_splits;
     if (len < min_len) len = (min_len + unit - 1) / unit * unit;
     *split_len = len;
@@ -380,7 +382,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         if (sh.n_q != sh0->n_q || sh.H != sh0->H || sh.H_kv != sh0->H_kv || sh.B != sh0->B) return CVATTN_ERR_BAD_ARGS;
         // one launch runs one kernel shape (e.g. a view too large for 32-bit offsets among
         // decode problems cannot join them)
-        if (sh.ks.wsplit != sh0->ks.wsplit || sh.ks.hp != sh0->ks.hp) return CVATTN_ERR_UNSUPPORTED;
+        if (sh.ks.wsplit != sh0->ks.wsplit) return CVATTN_ERR_UNSUPPORTED;
         work += split_work(sh);
     }
     if (table) table->resize(n);

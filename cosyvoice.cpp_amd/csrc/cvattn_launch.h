@@ -11,13 +11,12 @@ namespace cvattn {
 // tokens) or row-tiled (waves split the rows).
 struct FaKernelShape {
     bool wsplit;        // decode kernel (fa_decode.h)
-    int hp;             // kv heads per workgroup (decode kernel: 2 pairs heads of <= 8 rows)
     int nw;             // waves per workgroup
     int tstep;          // tokens per staged tile (per wave step for the decode kernel)
     int rows_per_group; // query rows per workgroup
     int max_splits;     // most token splits one workgroup can merge in-kernel
 };
-FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask);
+FaKernelShape fa_shape(int n_rows, bool small_views);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
 // Row-tiled attention over a transposed V (vtype T_VT_F32 / T_VT_F16), single calls.

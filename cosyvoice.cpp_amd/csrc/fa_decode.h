@@ -4,14 +4,14 @@
 // node of src/cosyvoice-kv-cache.cpp:383-384 in decode.
 //
 // The KV cache is streamed once, in whole ggml blocks.  A workgroup is 4 independent waves on
-// one (batch, kv-head group, token split); each wave walks its own run of tokens in steps of 32
-// token-heads and never waits for the other waves until the end.
+// one (batch, kv head, row group, token split); each wave walks its own run of tokens in steps
+// of 32 and never waits for the other waves until the end.
 //
 // Per wave step:
 //   * every lane loads one 32-dim block of K and one of V (16-byte buffer loads of whole blocks;
-//     64 lanes cover 16 consecutive tokens x 2 heads, or 32 tokens x 1 head, so a wave's loads
-//     are contiguous row runs), PD steps ahead of use;
-//   * the lane unpacks its blocks into a wave-private LDS tile of fp16 rows [token-head][64 dims]
+//     64 lanes cover 32 consecutive tokens of the head, so a wave's loads are contiguous runs),
+//     PD steps ahead of use;
+//   * the lane unpacks its blocks into a wave-private LDS tile of fp16 rows [token][64 dims]
 //     (K codes as "1024 + u", V codes exact) plus fp32 block scales;
 //   * S^T = K Q^T with v_mfma_f32_16x16x32_f16 (A = K rows read from the tile, B = Q^T in
 //     registers, split into fp16 hi + lo parts for fp32-accurate scores);
@@ -19,9 +19,6 @@
 //   * O^T += V^T P^T with v_mfma_f32_16x16x16_f16: the S^T accumulator of a 16-token tile is
 //     already the B operand of P^T, and ds_read_b64_tr_b16 reads V^T straight from the
 //     token-major V tile.
-// With HP = 2 the two kv heads of a pair share one 16-row tile: rows 0-7 are the query rows of
-// head 2j, rows 8-15 those of head 2j+1 (up to 8 rows each), and each head's MFMA runs with the
-// other head's Q^T / P^T columns zero, so softmax work is spent on 14 live rows of 16.
 //
 // Token splits: the waves of a workgroup merge their states in LDS; several workgroups of one
 // group write partials that the last one to arrive merges (prepared batches) or that
@@ -43,12 +40,9 @@ __host__ __device__ constexpr int dec_prefetch() {
     return blk_words<KT>() + blk_words<VT>() <= 16 ? 3 : blk_words<KT>() + blk_words<VT>() <= 32 ? 2 : 1;
 }
 
-// Query row of row slot `slot` (0..15) of a (kv-head group, row group); false if unused.
-template <int HP>
-__device__ __forceinline__ bool dec_row(const FaUniform &U, int khg, int rg, int slot, int &iq, int &hq) {
-    const int hs = HP == 2 ? slot >> 3 : 0;
-    const int rr = HP == 2 ? slot & 7 : rg * 16 + slot;
-    const int kh = khg * HP + hs;
+// Query row of row slot `slot` (0..15) of a (kv head, row group); false if unused.
+__device__ __forceinline__ bool dec_row(const FaUniform &U, int kh, int rg, int slot, int &iq, int &hq) {
+    const int rr = rg * 16 + slot;
     const bool ok = rr < U.n_rows;
     const int r = ok ? rr : 0;
     iq = r / U.G;
@@ -66,13 +60,13 @@ __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 // (slot, 4 dims).  Every O load is issued before any is used; (m, l) pairs are loaded once per
 // row (two splits per lane) and their weights shared through the wave-private `sw` row.
 // SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
-template <int HP, bool SC1>
+template <bool SC1>
 __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int khg,
                                           int rg, int bq, float *sw) {
     const int tid = threadIdx.x;
     const int r = tid >> 4, q = tid & 15, d0 = 4 * q;
     int iq, hq;
-    const bool ok = dec_row<HP>(U, khg, rg, r, iq, hq); // uniform over the row's 16 lanes
+    const bool ok = dec_row(U, khg, rg, r, iq, hq); // uniform over the row's 16 lanes
     constexpr int AUX = SC1 ? 16 : 0;
     const int nsp = dec_nsp(ns);
     const __amdgpu_buffer_rsrc_t rp =
@@ -108,10 +102,10 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
     *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
 }
 
-template <int KT, int VT, bool MASK, bool BATCH, int HP>
+template <int KT, int VT, bool MASK, bool BATCH>
 __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
-    constexpr int TS = 32 / HP;                // tokens per wave step
-    constexpr int NT = HP == 2 ? 1 : 2;        // 16-token score tiles per step
+    constexpr int TS = 32;                     // tokens per wave step
+    constexpr int NT = 2;                      // 16-token score tiles per step
     constexpr int PD = dec_prefetch<KT, VT>(); // steps in flight
     __shared__ __attribute__((aligned(16))) _Float16 sK[DEC_NW][32 * DEC_RS];
     __shared__ __attribute__((aligned(16))) _Float16 sV[DEC_NW][32 * DEC_RS];
@@ -120,8 +114,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 
     const FaUniform &U = args.u;
     FaProblem P;
-    // consecutive units (the kv-head groups of one token range, whose rows share cache lines)
-    // run on one XCD so each line is fetched into one L2 only
+    // consecutive units (the kv heads of one token range, whose rows share cache lines) run on
+    // one XCD so each line is fetched into one L2 only
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
     const int khg = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
@@ -137,26 +131,23 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int w_end = min(t_end, w_begin + wlen);
     const int nsteps = (max(0, w_end - w_begin) + TS - 1) / TS; // per wave
 
-    // this lane's block in every step: token lt of the step, row slot ls, 32-dim block lb
-    const int lt = HP == 2 ? lane >> 2 : lane >> 1;
-    const int ls = HP == 2 ? (lane >> 1) & 1 : lt >> 4;
+    // this lane's block in every step: token lt of the step (tile row lrow), 32-dim block lb
+    const int lt = lane >> 1;
     const int lb = lane & 1;
-    const int lrow = 16 * ls + (lt & 15);
-    const int kh0 = khg * HP;
-    gu8 *kbase = gptr(P.k) + (int64_t)kh0 * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
-    gu8 *vbase = gptr(P.v) + (int64_t)kh0 * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
+    const int lrow = lt;
+    gu8 *kbase = gptr(P.k) + (int64_t)khg * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
+    gu8 *vbase = gptr(P.v) + (int64_t)khg * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
     // the head rows this workgroup reads: loads of tokens >= n_kv fall outside and read 0
-    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + (int64_t)(HP - 1) * P.k_nb2 + 2 * dblk_bytes<KT>() : 0;
-    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + (int64_t)(HP - 1) * P.v_nb2 + 2 * dblk_bytes<VT>() : 0;
+    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
+    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>() : 0;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, kext);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, vext);
-    const int kvoff = lt * (int)P.k_nb1 + (HP == 2 ? ls * (int)P.k_nb2 : 0) + lb * dblk_bytes<KT>();
-    const int vvoff = lt * (int)P.v_nb1 + (HP == 2 ? ls * (int)P.v_nb2 : 0) + lb * dblk_bytes<VT>();
+    const int kvoff = lt * (int)P.k_nb1 + lb * dblk_bytes<KT>();
+    const int vvoff = lt * (int)P.v_nb1 + lb * dblk_bytes<VT>();
 
     // ---- this lane's query row (MFMA column `col`) and its Q operand (hi + lo fp16) ----
     int iq, hq;
-    const bool row_ok = dec_row<HP>(U, khg, rg, col, iq, hq);
-    const int hs = HP == 2 ? col >> 3 : 0; // head slot of this lane's row
+    const bool row_ok = dec_row(U, khg, rg, col, iq, hq);
     h8 qhi[2], qlo[2];
     float qsum[2];
     bool need_lo = false;
@@ -221,7 +212,6 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 
     _Float16 *tK = sK[wv], *tV = sV[wv];
     float(*tS)[2][32] = sS[wv];
-    const h4 z4 = {};
 
     for (int s0 = 0; s0 < nsteps; s0 += PD) {
 #pragma unroll
@@ -254,26 +244,16 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
                 f4 sc[NT];
 #pragma unroll
                 for (int s = 0; s < NT; s++) {
-                    // HP = 2: both heads' K rows against all 16 query rows; each lane keeps the
-                    // accumulator of its own row's head
                     f4 acc[2];
 #pragma unroll
                     for (int b = 0; b < 2; b++) {
                         const f4 ci = b ? cinit1 : cinit0;
-                        const h8 a0 = *(const h8 *)(tK + (16 * (HP == 2 ? 0 : s) + col) * DEC_RS + 32 * b + 8 * g);
+                        const h8 a0 = *(const h8 *)(tK + (16 * s + col) * DEC_RS + 32 * b + 8 * g);
                         f4 c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qhi[b], ci, 0, 0, 0);
                         if (need_lo) c0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[b], c0, 0, 0, 0);
-                        if constexpr (HP == 2) {
-                            const h8 a1 = *(const h8 *)(tK + (16 + col) * DEC_RS + 32 * b + 8 * g);
-                            f4 c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qhi[b], ci, 0, 0, 0);
-                            if (need_lo) c1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[b], c1, 0, 0, 0);
-                            // (element-wise selects: a select of whole vectors became a stack array)
-#pragma unroll
-                            for (int j = 0; j < 4; j++) c0[j] = hs ? c1[j] : c0[j];
-                        }
                         acc[b] = c0;
                     }
-                    const int sb = 16 * (HP == 2 ? hs : s) + 4 * g; // scale rows of these tokens
+                    const int sb = 16 * s + 4 * g; // scale rows of these tokens
                     if constexpr (is_quant(KT)) {
                         const f4 d0 = *(const f4 *)&tS[0][0][sb];
                         const f4 d1 = *(const f4 *)&tS[0][1][sb];
@@ -342,7 +322,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
                         p[j] = fast_exp2(sc[s][j] - m_use);
                         l_run += p[j];
                     }
-                    const int sb = 16 * (HP == 2 ? hs : s) + 4 * g;
+                    const int sb = 16 * s + 4 * g;
                     h4 pb[2];
 #pragma unroll
                     for (int b = 0; b < 2; b++) {
@@ -354,18 +334,14 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
                             corr[b] += t[0] + t[1] + t[2] + t[3];
                         }
                     }
+                    // V^T operand rows: tokens 4g..4g+3 of this tile, dims 16i + col
+                    const int vrow = 16 * s + 4 * g + (col >> 2);
 #pragma unroll
-                    for (int h = 0; h < HP; h++) {
-                        // V^T operand rows: tokens 4g..4g+3 of this tile, dims 16i + col
-                        const int vrow = 16 * (HP == 2 ? h : s) + 4 * g + (col >> 2);
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                (__attribute__((address_space(3))) short4_t *)(tV + vrow * DEC_RS + 16 * i + 4 * (col & 3)));
-                            const h4 a = __builtin_bit_cast(h4, raw);
-                            const h4 bop = (HP == 1 || hs == h) ? pb[i >> 1] : z4;
-                            oacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, bop, oacc[i], 0, 0, 0);
-                        }
+                    for (int i = 0; i < 4; i++) {
+                        const short4_t raw = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) short4_t *)(tV + vrow * DEC_RS + 16 * i + 4 * (col & 3)));
+                        const h4 a = __builtin_bit_cast(h4, raw);
+                        oacc[i] = __builtin_amdgcn_mfma_f32_16x16x16f16(a, pb[i >> 1], oacc[i], 0, 0, 0);
                     }
                 }
             }
@@ -449,13 +425,12 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         __syncthreads();
         if (!s_last) return;
-        dec_merge<HP, true>(U, P, part0, ns, khg, rg, bq, &sS[0][0][0][0]);
+        dec_merge<true>(U, P, part0, ns, khg, rg, bq, &sS[0][0][0][0]);
     }
 }
 
 // Single calls: merge the split partials the decode kernel wrote; one workgroup per group.
-template <int HP>
-__global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
+static __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
     __shared__ __attribute__((aligned(16))) float sw[16 * DEC_MERGE_CHUNK];
     const FaUniform &U = args.u;
     const FaProblem &P = args.p0;
@@ -463,7 +438,7 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
     const int rg = (int)(grp % U.n_rowgroups);
     const int khg = (int)((grp / U.n_rowgroups) % U.n_khg);
     const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.n_khg));
-    dec_merge<HP, false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, khg,
+    dec_merge<false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, khg,
                          rg, bq, sw);
 }
 

@@ -3,9 +3,8 @@
 
 namespace cvattn {
 
-static FaLaunchFn fa_pick_decode(int mask, int batch, int hp, int ki, int vi) {
-    if (mask) return fa_pick_decode_m1_h1(batch, ki, vi);
-    return hp == 2 ? fa_pick_decode_m0_h2(batch, ki, vi) : fa_pick_decode_m0_h1(batch, ki, vi);
+static FaLaunchFn fa_pick_decode(int mask, int batch, int ki, int vi) {
+    return mask ? fa_pick_decode_m1(batch, ki, vi) : fa_pick_decode_m0(batch, ki, vi);
 }
 FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_vt(int mask, int ki, int vti);
@@ -23,16 +22,14 @@ static int type_index(int t) {
     }
 }
 
-FaKernelShape fa_shape(int n_rows, int h_kv, bool small_views, bool mask) {
+FaKernelShape fa_shape(int n_rows, bool small_views) {
     FaKernelShape s;
     // decode-shaped kernel (fa_decode.h): <= 64 rows per kv head (up to 4 groups of 16, e.g. the
-    // 50 rows of a DiT streaming chunk) and K/V views addressable with 32-bit buffer offsets; kv
-    // heads are paired when each has <= 8 rows (the masked variant keeps one head per
-    // workgroup); everything else runs the row-tiled kernel
+    // 50 rows of a DiT streaming chunk) and K/V views addressable with 32-bit buffer offsets;
+    // everything else runs the row-tiled kernel
     s.wsplit = n_rows <= 64 && small_views;
-    s.hp = s.wsplit && n_rows <= 8 && h_kv % 2 == 0 && !mask ? 2 : 1;
     s.nw = 4;
-    s.tstep = s.wsplit ? 32 / s.hp : ROWS_TS;
+    s.tstep = s.wsplit ? 32 : ROWS_TS;
     s.rows_per_group = s.wsplit ? 16 : ROWS_ROWS;
     s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : ROWS_MERGE_MAX_SPLITS;
     return s;
@@ -42,7 +39,7 @@ hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bo
                      hipStream_t st) {
     const int ki = type_index(ktype), vi = type_index(vtype);
     if (ki < 0 || vi < 0) return hipErrorInvalidValue;
-    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, s.hp, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
+    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
     return fn(a, st);
 }
 
