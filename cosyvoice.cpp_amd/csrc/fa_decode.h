@@ -71,12 +71,14 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
     const int nsp = dec_nsp(ns);
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc((gu8 *)part0, (int64_t)(dec_ml_offset(ns) + 16 * nsp * 2) * 4);
+    // row slots past the group's rows were never written: their lanes load nothing
     u4 ov[DEC_MERGE_CHUNK];
 #pragma unroll
     for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        if (j < ns) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((r * ns + j) * 64 + d0) * 4, 0, AUX);
+        if (ok && j < ns) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((r * ns + j) * 64 + d0) * 4, 0, AUX);
     // lane q holds (m, l) of splits 2q and 2q+1
-    const u4 ml = __builtin_amdgcn_raw_buffer_load_b128(rp, (dec_ml_offset(ns) + (r * nsp + 2 * q) * 2) * 4, 0, AUX);
+    u4 ml = {0u, 0u, 0u, 0u};
+    if (ok) ml = __builtin_amdgcn_raw_buffer_load_b128(rp, (dec_ml_offset(ns) + (r * nsp + 2 * q) * 2) * 4, 0, AUX);
     const bool v0 = 2 * q < ns, v1 = 2 * q + 1 < ns;
     const float m0 = v0 ? as_f32(ml[0]) : -INFINITY, m1 = v1 ? as_f32(ml[2]) : -INFINITY;
     float M = fmaxf(m0, m1);
