@@ -313,3 +313,54 @@ def test_batch_prefill_with_masks(eng, orc, rng, cuda):
     for c in cases:
         want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
         check_close(host(c.dst), want, what="batch prefill")
+
+
+# ------------------------------------------------------------------------------------------
+# the benchmark configurations at their full sizes
+# ------------------------------------------------------------------------------------------
+def run_batch(eng, cases, masked=False):
+    probs = []
+    for c in cases:
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.dst = c.q_d, c.k_d, c.v_d, c.dst_d
+        if masked:
+            p.mask = c.mask_d
+        probs.append(p)
+    ws = workspace(eng.fa_batch_workspace(probs))
+    rc, plan = eng.fa_batch_prepare(probs, 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    return ws
+
+
+def test_config2_24_layer_step(eng, orc, cuda):
+    """Config 2 as the benchmark runs it: 24 layers x 4096 cached tokens, K q8_0 / V q4_0, one
+    prepared batch (one launch with in-kernel split merges), every layer against the oracle."""
+    rng = np.random.default_rng(2026)
+    cases = [llm_case(orc, rng, nq=1, nkv=4096, kt=Q8_0, vt=Q4_0, max_seq=4096) for _ in range(24)]
+    run_batch(eng, cases)
+    for i, c in enumerate(cases):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"config 2 layer {i}")
+
+
+def test_config3_serving_batch(eng, orc, cuda):
+    """Config 3: 16 sequences with kv_len drawn from U{256..8192} (the benchmark's seed), q8_0 K and
+    V, one layer's 16 problems in one launch."""
+    lens = np.random.default_rng(20261201).integers(256, 8193, 16)
+    rng = np.random.default_rng(33)
+    cases = [llm_case(orc, rng, nq=1, nkv=int(n), kt=Q8_0, vt=Q8_0, max_seq=int(n)) for n in lens]
+    run_batch(eng, cases)
+    for c, n in zip(cases, lens):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"config 3 kv_len {n}")
+
+
+def test_config4_prefill_1024_causal(eng, orc, cuda):
+    """Config 4: 1024 query tokens over 1024 f16 cached tokens with the causal mask, Q/K/V scaled
+    by 0.5 (src/cosyvoice-llm.cpp:20-29,101-108)."""
+    rng = np.random.default_rng(44)
+    mask = orc.causal_mask(1024, 1024)
+    c = llm_case(orc, rng, nq=1024, nkv=1024, kt=F16, vt=F16, max_seq=1024, mask=mask, qscale=0.5, kvscale=0.5)
+    run_case(eng, orc, c, what="config 4 prefill")
