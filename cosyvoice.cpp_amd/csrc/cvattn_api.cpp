@@ -137,11 +137,6 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 // split only when their row groups alone cannot fill the chip.  `work` is the launch-wide sum
 // of B*n_khg*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
 constexpr int64_t kTargetWaves = 4096;
-// Most token splits of a decode-shaped group: the last-arriving workgroup loads every split's
-// partial from one CU, and past 16 splits that merge costs more than the streaming it shortens
-// (24-layer 4096-token q8_0/q4_0 step and the one-layer launch both measured best at 16).
-constexpr int kDecodeMaxSplits = 16;
-
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
     const int tstep = sh.ks.tstep;
     int len;
@@ -169,7 +164,7 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
     }
     const int unit = sh.ks.wsplit ? tstep * sh.ks.nw : tstep;
     // never more splits than the in-kernel merge takes in one pass
-    const int max_splits = sh.ks.wsplit ? std::min(sh.ks.max_splits, kDecodeMaxSplits) : sh.ks.max_splits;
+    const int max_splits = sh.ks.max_splits;
     const int min_len = (n_kv + max_splits - 1) / max_splits;
     if (len < min_len) len = (min_len + unit - 1) / unit * unit;
     *split_len = len;

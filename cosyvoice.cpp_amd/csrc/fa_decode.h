@@ -32,7 +32,10 @@ namespace cvattn {
 constexpr int DEC_NW = 4;      // waves per workgroup
 constexpr int DEC_RS = 72;     // halfs per canonical LDS row (64 dims + pad): 144 B
 constexpr float DEC_RESCALE_LOG2 = 8.0f;
-constexpr int DEC_MERGE_CHUNK = 32; // most token splits per group (merged in one pass)
+// Most token splits per group, merged in one pass by the last-arriving workgroup.  The merge's
+// loads are issued by one CU, and past 16 splits it costs more than the streaming it shortens
+// (the 24-layer 4096-token q8_0/q4_0 step and the one-layer launch both measured best at 16).
+constexpr int DEC_MERGE_CHUNK = 16;
 
 // Steps whose raw blocks are in flight at once (register budget per type pair).
 template <int KT, int VT>
@@ -57,12 +60,13 @@ __device__ __forceinline__ int dec_ml_offset(int ns) { return 16 * ns * 64; }
 __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 
 // Merge the ns (<= DEC_MERGE_CHUNK) split partials of one group's 16 row slots into dst; thread =
-// (slot, 4 dims).  Every O load is issued before any is used; (m, l) pairs are loaded once per
-// row (two splits per lane) and their weights shared through the wave-private `sw` row.
+// (slot, 4 dims).  Every load is issued before any is used, and every lane of a row loads all of
+// the row's (m, l) pairs (the same bytes for the row's 16 lanes), so the weights need no
+// cross-lane exchange: one round trip to memory, then VALU only.
 // SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
 template <bool SC1>
 __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int khg,
-                                          int rg, int bq, float *sw) {
+                                          int rg, int bq) {
     const int tid = threadIdx.x;
     const int r = tid >> 4, q = tid & 15, d0 = 4 * q;
     int iq, hq;
@@ -71,35 +75,35 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
     const int nsp = dec_nsp(ns);
     const __amdgpu_buffer_rsrc_t rp =
         make_rsrc((gu8 *)part0, (int64_t)(dec_ml_offset(ns) + 16 * nsp * 2) * 4);
-    // row slots past the group's rows were never written: their lanes load nothing
+    // Loads of row slots past the group's rows (never written) and of splits past ns point
+    // outside the resource: they return 0 without a memory access, and need no branch.
+    constexpr int kOutside = 0x7ffffff0;
     u4 ov[DEC_MERGE_CHUNK];
+    u4 ml[DEC_MERGE_CHUNK / 2]; // (m, l) of splits 2j and 2j+1
 #pragma unroll
     for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        if (ok && j < ns) ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ((r * ns + j) * 64 + d0) * 4, 0, AUX);
-    // lane q holds (m, l) of splits 2q and 2q+1
-    u4 ml = {0u, 0u, 0u, 0u};
-    if (ok) ml = __builtin_amdgcn_raw_buffer_load_b128(rp, (dec_ml_offset(ns) + (r * nsp + 2 * q) * 2) * 4, 0, AUX);
-    const bool v0 = 2 * q < ns, v1 = 2 * q + 1 < ns;
-    const float m0 = v0 ? as_f32(ml[0]) : -INFINITY, m1 = v1 ? as_f32(ml[2]) : -INFINITY;
-    float M = fmaxf(m0, m1);
+        ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ok && j < ns ? ((r * ns + j) * 64 + d0) * 4 : kOutside, 0,
+                                                      AUX);
 #pragma unroll
-    for (int o = 1; o < 16; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+    for (int j = 0; j < DEC_MERGE_CHUNK / 2; j++)
+        ml[j] = __builtin_amdgcn_raw_buffer_load_b128(
+            rp, ok && 2 * j < ns ? (dec_ml_offset(ns) + (r * nsp + 2 * j) * 2) * 4 : kOutside, 0, AUX);
+    if (!ok) return;
+    float M = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+        if (j < ns) M = fmaxf(M, as_f32(ml[j >> 1][2 * (j & 1)]));
     const float Mu = M == -INFINITY ? 0.0f : M;
-    const float w0 = m0 == -INFINITY ? 0.0f : fast_exp2(m0 - Mu);
-    const float w1 = m1 == -INFINITY ? 0.0f : fast_exp2(m1 - Mu);
-    float L = (v0 ? as_f32(ml[1]) * w0 : 0.0f) + (v1 ? as_f32(ml[3]) * w1 : 0.0f);
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) L += __shfl_xor(L, o);
-    float *row_w = sw + r * DEC_MERGE_CHUNK;
-    *(float2 *)&row_w[2 * q] = float2{w0, w1};
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    float L = 0.0f;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        if (j < ns) acc += as_f4(ov[j]) * row_w[j];
-    if (!ok) return;
+        if (j < ns) {
+            const float m = as_f32(ml[j >> 1][2 * (j & 1)]);
+            const float w = m == -INFINITY ? 0.0f : fast_exp2(m - Mu);
+            L += as_f32(ml[j >> 1][2 * (j & 1) + 1]) * w;
+            acc += as_f4(ov[j]) * w;
+        }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
 }
@@ -427,13 +431,12 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         __syncthreads();
         if (!s_last) return;
-        dec_merge<true>(U, P, part0, ns, khg, rg, bq, &sS[0][0][0][0]);
+        dec_merge<true>(U, P, part0, ns, khg, rg, bq);
     }
 }
 
 // Single calls: merge the split partials the decode kernel wrote; one workgroup per group.
 static __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
-    __shared__ __attribute__((aligned(16))) float sw[16 * DEC_MERGE_CHUNK];
     const FaUniform &U = args.u;
     const FaProblem &P = args.p0;
     const int64_t grp = blockIdx.x;
@@ -441,7 +444,7 @@ static __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
     const int khg = (int)((grp / U.n_rowgroups) % U.n_khg);
     const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.n_khg));
     dec_merge<false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, khg,
-                         rg, bq, sw);
+                     rg, bq);
 }
 
 } // namespace cvattn
