@@ -53,7 +53,6 @@ bool kv_ok(const cvattn_tensor *t) {
 struct FaShape {
     int n_q, H, H_kv, G, B, n_kv;
     int n_rows, n_rowgroups;
-    int n_khg; // kv-head groups (H_kv / kv heads per workgroup)
     FaKernelShape ks;
 };
 
@@ -108,13 +107,12 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     sh->B = (int)q->ne[3];
     sh->n_kv = (int)k->ne[1];
     sh->n_rows = sh->n_q * sh->G;
-    // 32-bit buffer offsets cover the K/V rows a decode workgroup reads (two heads when paired)
+    // 32-bit buffer offsets cover the rows of one K/V head a decode workgroup reads
     const int64_t lim31 = ((int64_t)1 << 31) - 1;
-    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] + 2 * (int64_t)k->nb[2] < lim31 &&
-                       (vt || (int64_t)v->ne[1] * (int64_t)v->nb[1] + 2 * (int64_t)v->nb[2] < lim31);
+    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] < lim31 &&
+                       (vt || (int64_t)v->ne[1] * (int64_t)v->nb[1] < lim31);
     sh->ks = fa_shape(sh->n_rows, small && !vt);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
-    sh->n_khg = sh->H_kv;
     return CVATTN_OK;
 }
 
@@ -135,7 +133,7 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 // the whole launch has about kTargetWaves waves in flight (half that when each kv head has
 // several row groups, which already multiply the workgroups reading a head); row-tiled problems
 // split only when their row groups alone cannot fill the chip.  `work` is the launch-wide sum
-// of B*n_khg*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
+// of B*H_kv*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
 constexpr int64_t kTargetWaves = 4096;
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
     const int tstep = sh.ks.tstep;
@@ -172,7 +170,7 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
 }
 
 int64_t split_work(const FaShape &sh) {
-    const int64_t groups = (int64_t)sh.B * sh.n_khg * sh.n_rowgroups;
+    const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
     return sh.ks.wsplit ? groups * sh.n_kv : groups;
 }
 
@@ -222,8 +220,7 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
     u.q_f16 = q_type == T_F16 ? 1 : 0;
     u.scale = scale;
     u.scale_log2 = scale * 1.4426950408889634f;
-    u.n_khg = sh.n_khg;
-    u.div_khg = make_fastdiv((uint32_t)sh.n_khg);
+    u.div_hkv = make_fastdiv((uint32_t)sh.H_kv);
     u.div_rowgroups = make_fastdiv((uint32_t)sh.n_rowgroups);
     u.div_upp = make_fastdiv(1);
 }
@@ -232,7 +229,7 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
 constexpr int64_t kMaxUnits = ((int64_t)1 << 31) - 1;
 
 int64_t slots_per_split(const FaShape &sh) {
-    return (int64_t)sh.B * sh.n_khg * sh.n_rowgroups * sh.ks.rows_per_group;
+    return (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * sh.ks.rows_per_group;
 }
 
 // Plan for a single problem: splits and the workspace size.
@@ -316,7 +313,7 @@ static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvat
     a.p0.div_splits = make_fastdiv((uint32_t)pl.n_splits);
     a.p0.split_len = pl.split_len;
     a.u.n_problems = 1;
-    a.u.total_units = (int64_t)pl.sh.B * pl.sh.n_khg * pl.sh.n_rowgroups * pl.n_splits;
+    a.u.total_units = (int64_t)pl.sh.B * pl.sh.H_kv * pl.sh.n_rowgroups * pl.n_splits;
     if (a.u.total_units > kMaxUnits) return CVATTN_ERR_UNSUPPORTED;
     a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
     a.u.partials = (float *)ws;
@@ -397,7 +394,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         fp.part_begin = part;
         fp.row_begin = row;
         fp.cnt_begin = cnt;
-        const int64_t groups = (int64_t)sh.B * sh.n_khg * sh.n_rowgroups;
+        const int64_t groups = (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
         unit += groups * ns;
         if (ns > 1) {
             part += slots_per_split(sh) * ns;

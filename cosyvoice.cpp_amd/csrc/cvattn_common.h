@@ -105,8 +105,7 @@ struct FaUniform {
     float scale_log2;    // scale * log2(e)
     float empty_row;     // output of a row whose keys are all masked: 0 (flash attention), or
                          // NaN as ggml's soft_max gives it (the non-flash-attention path)
-    int32_t n_khg;       // kv-head groups per batch entry (H_kv / kv heads per workgroup)
-    FastDiv div_khg, div_rowgroups, div_upp; // n_khg, n_rowgroups, units_per_problem
+    FastDiv div_hkv, div_rowgroups, div_upp; // H_kv, n_rowgroups, units_per_problem
     int64_t units_per_problem; // > 0 when every problem has this many workgroup units
     int64_t total_units;
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)

@@ -53,7 +53,7 @@ __device__ __forceinline__ bool dec_row(const FaUniform &U, int kh, int rg, int 
     return ok;
 }
 
-// Split partials of one (batch, kv-head group, row group): O[16 row slots][ns][64] followed by
+// Split partials of one (batch, kv head, row group): O[16 row slots][ns][64] followed by
 // (m, l)[16 row slots][nsp][2] with nsp = ns rounded up to even (16-byte rows); this fits in the
 // 16 * ns * PART_STRIDE floats the host reserves per group.
 __device__ __forceinline__ int dec_ml_offset(int ns) { return 16 * ns * 64; }
@@ -65,12 +65,12 @@ __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 // cross-lane exchange: one round trip to memory, then VALU only.
 // SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
 template <bool SC1>
-__device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int khg,
+__device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int kh,
                                           int rg, int bq) {
     const int tid = threadIdx.x;
     const int r = tid >> 4, q = tid & 15, d0 = 4 * q;
     int iq, hq;
-    const bool ok = dec_row(U, khg, rg, r, iq, hq); // uniform over the row's 16 lanes
+    const bool ok = dec_row(U, kh, rg, r, iq, hq); // uniform over the row's 16 lanes
     constexpr int AUX = SC1 ? 16 : 0;
     const int nsp = dec_nsp(ns);
     const __amdgpu_buffer_rsrc_t rp =
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     // consecutive units (the kv heads of one token range, whose rows share cache lines) run on
     // one XCD so each line is fetched into one L2 only
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
-    const int khg = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
+    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
 
     // the wave index is uniform per wave: readfirstlane lets the token range, step loop and
     // buffer soffsets live in scalar registers
@@ -141,8 +141,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int lt = lane >> 1;
     const int lb = lane & 1;
     const int lrow = lt;
-    gu8 *kbase = gptr(P.k) + (int64_t)khg * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
-    gu8 *vbase = gptr(P.v) + (int64_t)khg * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
+    gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
+    gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
     // the head rows this workgroup reads: loads of tokens >= n_kv fall outside and read 0
     const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
     const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>() : 0;
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 
     // ---- this lane's query row (MFMA column `col`) and its Q operand (hi + lo fp16) ----
     int iq, hq;
-    const bool row_ok = dec_row(U, khg, rg, col, iq, hq);
+    const bool row_ok = dec_row(U, kh, rg, col, iq, hq);
     h8 qhi[2], qlo[2];
     float qsum[2];
     bool need_lo = false;
@@ -390,7 +390,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     }
     // wave wv now owns dims 16*wv + 4g + j of row slot `col`
     const int ns = P.n_splits;
-    const int64_t grp = ((int64_t)bq * U.n_khg + khg) * U.n_rowgroups + rg;
+    const int64_t grp = ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
     const int64_t slot0 = P.part_begin + grp * 16 * ns;
     if (ns == 1) {
         if (row_ok) {
@@ -431,7 +431,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         __syncthreads();
         if (!s_last) return;
-        dec_merge<true>(U, P, part0, ns, khg, rg, bq);
+        dec_merge<true>(U, P, part0, ns, kh, rg, bq);
     }
 }
 
@@ -441,9 +441,9 @@ static __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
     const FaProblem &P = args.p0;
     const int64_t grp = blockIdx.x;
     const int rg = (int)(grp % U.n_rowgroups);
-    const int khg = (int)((grp / U.n_rowgroups) % U.n_khg);
-    const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.n_khg));
-    dec_merge<false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, khg,
+    const int kh = (int)((grp / U.n_rowgroups) % U.H_kv);
+    const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.H_kv));
+    dec_merge<false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, kh,
                      rg, bq);
 }
 

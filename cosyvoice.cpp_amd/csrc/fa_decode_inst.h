@@ -15,7 +15,7 @@ hipError_t launch_decode(const FaArgs &a, hipStream_t st) {
     if (e != hipSuccess) return e;
     // single calls merge split partials with a second launch; prepared batches merge in-kernel
     if (!BATCH && a.p0.n_splits > 1) {
-        const int64_t groups = (int64_t)a.u.B * a.u.n_khg * a.u.n_rowgroups;
+        const int64_t groups = (int64_t)a.u.B * a.u.H_kv * a.u.n_rowgroups;
         hipLaunchKernelGGL(dec_combine_kernel, dim3((unsigned)groups), dim3(256), 0, st, a);
         e = hipGetLastError();
     }

@@ -67,10 +67,10 @@ __device__ __forceinline__ int find_problem_wave(const FaProblem *table, int n, 
     return cnt - 1;
 }
 
-// Position of a workgroup unit inside its problem: unit = ((bq*n_splits + split)*n_khg + khg)*
-// n_rowgroups + rg, counted from the problem's unit_begin (khg: kv-head group, one kv head
-// unless the decode kernel pairs heads).  Row groups are innermost so that the units of one XCD
-// (see xcd_unit) share the K/V of few heads in that XCD's L2.
+// Position of a workgroup unit inside its problem: unit = ((bq*n_splits + split)*H_kv + kh)*
+// n_rowgroups + rg, counted from the problem's unit_begin.  Row groups are innermost, then kv
+// heads, so that the units of one XCD (see xcd_unit) share the K/V rows of few heads in that
+// XCD's L2.
 struct UnitPos {
     int kh, rg, split, bq;
 };
@@ -92,8 +92,8 @@ __device__ __forceinline__ UnitPos locate_unit(const FaArgs &args, uint32_t unit
     uint32_t t = fdiv(ul, U.div_rowgroups);
     r.rg = (int)(ul - t * (uint32_t)U.n_rowgroups);
     ul = t;
-    t = fdiv(ul, U.div_khg);
-    r.kh = (int)(ul - t * (uint32_t)U.n_khg);
+    t = fdiv(ul, U.div_hkv);
+    r.kh = (int)(ul - t * (uint32_t)U.H_kv);
     ul = t;
     t = fdiv(ul, P.div_splits);
     r.split = (int)(ul - t * (uint32_t)P.n_splits);
