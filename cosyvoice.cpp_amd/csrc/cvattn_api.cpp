@@ -18,7 +18,7 @@ using namespace cvattn;
 
 namespace {
 
-constexpr int kRowsPerCu = 2; // resident row-tiled workgroups per CU (register bound)
+constexpr int kRowsPerCu = 3; // resident row-tiled workgroups per CU (register bound)
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int cu_count() {
@@ -135,6 +135,9 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 // split only when their row groups alone cannot fill the chip.  `work` is the launch-wide sum
 // of B*H_kv*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
 constexpr int64_t kTargetWaves = 4096;
+// row-tiled kernel cost terms (MI355X, measured): one 64-token tile of a workgroup, and the fixed
+// cost of a split (partial stores, arrival counter, last-arrival merge)
+constexpr double kTileUs = 0.85, kMergeUs = 3.4;
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
     const int tstep = sh.ks.tstep;
     int len;
@@ -145,9 +148,11 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
         len = (int)wlen * sh.ks.nw;
     } else {
-        // Split only when the row groups leave most resident workgroup slots idle: every
-        // split writes (and the merge reads back) a full-size fp32 partial of its rows, which
-        // costs more than a partly idle last round of workgroups (DiT at T=1500 measured).
+        // Split only when the row groups leave most resident workgroup slots idle AND the
+        // shorter key run pays for the partials: every split writes (and the merge reads back) a
+        // full fp32 partial of each of its rows through agent-coherent stores and loads, which
+        // measured ~0.9 TB/s plus ~3.4 us, against ~0.85 us per 64-token tile of a workgroup
+        // (1024-token prefill: 16.7 us unsplit vs 21.8 / 24.4 us with 2 / 3 splits).
         const int min_split = 256;
         const int64_t base = std::max<int64_t>(1, work);
         const int64_t slots = kRowsPerCu * cu_count();
@@ -156,6 +161,13 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
             want = (int)((slots + base - 1) / base);
             want = std::min(want, std::max(1, (n_kv + min_split - 1) / min_split));
             want = std::min(want, sh.ks.max_splits);
+            if (want > 1) {
+                const double tiles = (double)((n_kv + tstep - 1) / tstep);
+                const double part_us = (double)want * (double)base * sh.ks.rows_per_group * PART_STRIDE * 4 / 0.9e6;
+                const double t_one = tiles * kTileUs;
+                const double t_split = std::ceil(tiles / want) * kTileUs + kMergeUs + part_us;
+                if (t_split >= t_one) want = 1;
+            }
         }
         len = (n_kv + want - 1) / want;
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);

@@ -4,10 +4,10 @@
 // attention kernels share (problem lookup, workgroup decomposition, split merges).
 //
 // Rows.  For one (batch b, kv head kh) the rows are the n_q * G query rows sharing kh
-// (G = H / H_kv), ordered r = i * G + g (query i, q head kh*G + g).  A wave owns two sets of 16
-// rows (the 16 columns of its MFMA tiles), so each K or V operand read from LDS feeds two MFMAs.
-// A workgroup is 4 waves (128 rows) sharing 64-token K/V tiles that are staged once per step
-// into LDS, double-buffered: while the waves compute tile s, the
+// (G = H / H_kv), ordered r = i * G + g (query i, q head kh*G + g).  A wave owns ROWS_SETS sets
+// of 16 rows (the 16 columns of its MFMA tiles); each K or V operand read from LDS feeds one MFMA
+// per set.  A workgroup is 4 waves (64 rows with one set) sharing 64-token K/V tiles that are
+// staged once per step into LDS, double-buffered: while the waves compute tile s, the
 // tile s+1 is unpacked into the other buffer from registers loaded two steps ahead, so a step
 // has one barrier.
 //
@@ -37,7 +37,9 @@
 namespace cvattn {
 
 constexpr int ROWS_NW = 4;          // waves per workgroup
-constexpr int ROWS_SETS = 2;        // 16-row sets per wave (sharing every K and V operand read)
+constexpr int ROWS_SETS = 1;        // 16-row sets per wave (a set shares every K and V operand read);
+                                    // one set: 64-row workgroups, 3 resident per CU (138 VGPRs), measured
+                                    // faster than two sets (128-row workgroups, 2 per CU) for prefill and DiT
 constexpr int ROWS_TS = 64;         // tokens per staged tile
 constexpr int ROWS_RS = 72;         // halfs per LDS tile row (64 dims + pad)
 constexpr int ROWS_ROWS = 16 * ROWS_SETS * ROWS_NW;

@@ -157,18 +157,19 @@ def test_rope_argument_checks(eng):
 
 def test_nonfa_argument_checks(eng):
     """The transposed-V entry: the V cache must be f32/f16 with tokens contiguous and Dv = 64."""
-    q, k, _, dst = llm(n_kv=300, kt=Q8_0)
+    n = 2000    # long enough that the decode rows are split over tokens
+    q, k, _, dst = llm(n_kv=n, kt=Q8_0)
     max_seq = 4096
-    vt = cvattn.tensor(FAKE, F16, [300, 64, 2, 1], [2, 2 * max_seq, 2 * max_seq * 64, 2 * max_seq * 128])
+    vt = cvattn.tensor(FAKE, F16, [n, 64, 2, 1], [2, 2 * max_seq, 2 * max_seq * 64, 2 * max_seq * 128])
     assert eng.supports_attn_nonfa(q, k, vt, None)
-    assert eng.attn_nonfa_workspace(q, k, vt, None) > 0          # decode rows split over tokens
-    vq = cvattn.tensor(FAKE, Q8_0, [300, 64, 2, 1], [34, 34 * max_seq, 34 * max_seq * 64, 34 * max_seq * 128])
+    assert eng.attn_nonfa_workspace(q, k, vt, None) > 0
+    vq = cvattn.tensor(FAKE, Q8_0, [n, 64, 2, 1], [34, 34 * max_seq, 34 * max_seq * 64, 34 * max_seq * 128])
     assert not eng.supports_attn_nonfa(q, k, vq, None)
     assert eng.attn_nonfa(q, k, vq, None, dst, 0.125) == cvattn.ERR_UNSUPPORTED
-    vbad = cvattn.tensor(FAKE, F16, [299, 64, 2, 1], list(vt.nb))              # n_kv mismatch
+    vbad = cvattn.tensor(FAKE, F16, [n - 1, 64, 2, 1], list(vt.nb))            # n_kv mismatch
     assert eng.attn_nonfa(q, k, vbad, None, dst, 0.125) == cvattn.ERR_BAD_ARGS
-    v32 = cvattn.tensor(FAKE, F16, [300, 32, 2, 1], list(vt.nb))               # Dv 32
+    v32 = cvattn.tensor(FAKE, F16, [n, 32, 2, 1], list(vt.nb))                 # Dv 32
     assert eng.attn_nonfa(q, k, v32, None, dst, 0.125) == cvattn.ERR_UNSUPPORTED
-    vstr = cvattn.tensor(FAKE, F16, [300, 64, 2, 1], [4] + list(vt.nb)[1:])    # tokens not contiguous
+    vstr = cvattn.tensor(FAKE, F16, [n, 64, 2, 1], [4] + list(vt.nb)[1:])      # tokens not contiguous
     assert eng.attn_nonfa(q, k, vstr, None, dst, 0.125) == cvattn.ERR_BAD_ARGS
     assert eng.attn_nonfa(q, k, vt, None, dst, 0.125, 0, 0) == cvattn.ERR_WORKSPACE_TOO_SMALL

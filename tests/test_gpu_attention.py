@@ -315,6 +315,27 @@ def test_batch_prefill_with_masks(eng, orc, rng, cuda):
         check_close(host(c.dst), want, what="batch prefill")
 
 
+def test_short_prefill_over_long_cache_splits(eng, orc, rng, cuda):
+    """12 new tokens over a 3000-token q8_0/q4_0 cache: 84 rows per kv head run in the row-tiled
+    kernel, and so few row groups over so many keys are split over tokens -- merged by a second
+    launch for a single call and by the last-arriving workgroup in a prepared batch."""
+    nq, nkv = 12, 3000
+    mask = orc.causal_mask(nq, nkv)
+    c = llm_case(orc, rng, nq=nq, nkv=nkv, kt=Q8_0, vt=Q4_0, max_seq=nkv + 8, mask=mask, qscale=0.5)
+    assert eng.flash_attn_ext_workspace(c.q_d, c.k_d, c.v_d, c.mask_d) > 0   # split over tokens
+    _, single, _ = run_case(eng, orc, c, what="short prefill, single call")
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.mask, p.dst = c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d
+    c.dst.fill_(float("nan"))
+    ws = workspace(eng.fa_batch_workspace([p]))
+    rc, plan = eng.fa_batch_prepare([p], 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    for _ in range(2):   # the arrival counters reset themselves
+        assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    check_close(host(c.dst), single, max_abs=1e-5, mean_abs=1e-6, what="short prefill, batch vs single")
+
+
 # ------------------------------------------------------------------------------------------
 # the benchmark configurations at their full sizes
 # ------------------------------------------------------------------------------------------
