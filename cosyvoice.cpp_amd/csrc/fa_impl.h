@@ -41,7 +41,12 @@ constexpr int ROWS_SETS = 1;        // 16-row sets per wave (a set shares every 
                                     // one set: 64-row workgroups, 3 resident per CU (138 VGPRs), measured
                                     // faster than two sets (128-row workgroups, 2 per CU) for prefill and DiT
 constexpr int ROWS_TS = 64;         // tokens per staged tile
-constexpr int ROWS_RS = 72;         // halfs per LDS tile row (64 dims + pad)
+// halfs per LDS row of the token-major K and V tiles (64 dims + pad), and of the dim-major
+// transposed-V tile.  The pad sets which LDS banks the operand reads of a wave hit together;
+// measured on the DiT call (K / V row halfs): 72/72 43.8-44.7 us, 80/80 42.8-43.0, 80/88
+// 42.6-43.3, 88/80 44.1, 96/96 50.8, 64/80 52.6.
+constexpr int ROWS_RS = 80;
+constexpr int ROWS_RS_VT = 72;
 constexpr int ROWS_ROWS = 16 * ROWS_SETS * ROWS_NW;
 constexpr float ROWS_RESCALE_LOG2 = 8.0f;
 // the two K tile buffers double as the split-merge scratch (2 * ROWS * n_splits floats)
@@ -174,10 +179,11 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 
 template <int KT, int VT, bool MASK, bool BATCH>
 __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
-    constexpr int TS = ROWS_TS, RS = ROWS_RS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
+    constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
+    constexpr int RSK = ROWS_RS, RSV = is_vt(VT) ? ROWS_RS_VT : ROWS_RS;
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][TS * RS];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TS * RS];
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][TS * RSK];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TS * RSV];
     __shared__ __attribute__((aligned(16))) float sS[2][4][2][TS]; // {kd, km, vd, vm} x block x token
 
     const FaUniform &U = args.u;
@@ -318,7 +324,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     auto write_tile = [&](const RawBuf<W> &r, int buf, int t0) {
         float d, m;
         if (stage_k) {
-            blk_stage<KT, false>(r, sK[buf] + st_tok * RS + 32 * st_b);
+            blk_stage<KT, false>(r, sK[buf] + st_tok * RSK + 32 * st_b);
             blk_scales<KT>(r, d, m);
             sS[buf][0][st_b][st_tok] = d * smul;
             if constexpr (has_min(KT)) sS[buf][1][st_b][st_tok] = m * smul;
@@ -328,7 +334,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
             const int nvalid = P.n_kv - t0 - VCH * vt_tc; // valid tokens of each run
 #pragma unroll
             for (int i = 0; i < VNCH; i++) {
-                _Float16 *dst = sV[buf] + (vt_d0 + VDSTEP * i) * RS + VCH * vt_tc;
+                _Float16 *dst = sV[buf] + (vt_d0 + VDSTEP * i) * RSV + VCH * vt_tc;
                 if constexpr (VT == T_VT_F16) {
                     u4 w = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
                     if (t0 + TS > P.n_kv) { // uniform: the cache's last tile
@@ -345,7 +351,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 }
             }
         } else {
-            blk_stage<VT, true>(r, sV[buf] + st_tok * RS + 32 * st_b);
+            blk_stage<VT, true>(r, sV[buf] + st_tok * RSV + 32 * st_b);
             blk_scales<VT>(r, d, m);
             sS[buf][2][st_b][st_tok] = d;
             if constexpr (has_min(VT)) sS[buf][3][st_b][st_tok] = m;
@@ -400,8 +406,8 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         h8 ka[NTILE][2];
 #pragma unroll
         for (int tt = 0; tt < NTILE; tt++) {
-            ka[tt][0] = *(const h8 *)&cK[(16 * tt + col) * RS + 8 * g];
-            ka[tt][1] = *(const h8 *)&cK[(16 * tt + col) * RS + 32 + 8 * g];
+            ka[tt][0] = *(const h8 *)&cK[(16 * tt + col) * RSK + 8 * g];
+            ka[tt][1] = *(const h8 *)&cK[(16 * tt + col) * RSK + 32 + 8 * g];
         }
         // the lo MFMAs are a uniform choice per launch; each choice is one straight-line block
         auto qk = [&](auto lo_c) {
@@ -548,16 +554,16 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 h4 lo, hi;
                 if constexpr (VTR) {
                     // dim-major tile: dim 16i+col, tokens 4g..4g+3 and 16+4g..16+4g+3 of the 32
-                    const _Float16 *va = cV + (16 * i + col) * RS + 32 * kb + 4 * g;
+                    const _Float16 *va = cV + (16 * i + col) * RSV + 32 * kb + 4 * g;
                     lo = *(const h4 *)va;
                     hi = *(const h4 *)(va + 16);
                 } else {
-                    const _Float16 *va = cV + vrow * RS + 16 * i + 4 * (col & 3);
+                    const _Float16 *va = cV + vrow * RSV + 16 * i + 4 * (col & 3);
                     lo = __builtin_bit_cast(
                         h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) short4_t *)va));
                     hi = __builtin_bit_cast(
                         h4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                (__attribute__((address_space(3))) short4_t *)(va + 16 * RS)));
+                                (__attribute__((address_space(3))) short4_t *)(va + 16 * RSV)));
                 }
                 const h8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
