@@ -139,7 +139,8 @@ constexpr int64_t kTargetWaves = 4096;
 // cost of a split (partial stores, arrival counter, last-arrival merge)
 constexpr double kTileUs = 0.85, kMergeUs = 3.4;
 void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
-    const int tstep = sh.ks.tstep;
+    // row-tiled with two key halves: 128-token steps
+    const int tstep = sh.ks.wsplit ? sh.ks.tstep : sh.ks.tstep * sh.ks.kh;
     int len;
     if (sh.ks.wsplit) {
         // tokens per wave: a multiple of the wave step
@@ -155,17 +156,18 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         // (1024-token prefill: 16.7 us unsplit vs 21.8 / 24.4 us with 2 / 3 splits).
         const int min_split = 256;
         const int64_t base = std::max<int64_t>(1, work);
-        const int64_t slots = kRowsPerCu * cu_count();
+        const int64_t slots = (sh.ks.kh == 2 ? 1 : kRowsPerCu) * cu_count(); // two halves: 1 per CU (90 KB LDS)
         int want = 1;
         if (2 * base < slots) {
             want = (int)((slots + base - 1) / base);
             want = std::min(want, std::max(1, (n_kv + min_split - 1) / min_split));
             want = std::min(want, sh.ks.max_splits);
             if (want > 1) {
-                const double tiles = (double)((n_kv + tstep - 1) / tstep);
+                const double tiles = (double)((n_kv + tstep - 1) / tstep); // steps of tstep tokens
+                const double step_us = kTileUs * tstep / sh.ks.tstep / sh.ks.kh; // halves run side by side
                 const double part_us = (double)want * (double)base * sh.ks.rows_per_group * PART_STRIDE * 4 / 0.9e6;
-                const double t_one = tiles * kTileUs;
-                const double t_split = std::ceil(tiles / want) * kTileUs + kMergeUs + part_us;
+                const double t_one = tiles * step_us;
+                const double t_split = std::ceil(tiles / want) * step_us + kMergeUs + part_us;
                 if (t_split >= t_one) want = 1;
             }
         }
@@ -251,10 +253,18 @@ struct SinglePlan {
     size_t ws_bytes;
 };
 
+// Two key halves per row-tiled workgroup when the row groups alone would leave CUs idle (one
+// 8-wave workgroup per CU then runs each row set's key range in two halves); not for the
+// transposed-V form, whose dim-major tile holds one 64-token step.
+void choose_kh(FaShape &sh, int64_t groups, bool vt) {
+    sh.ks.kh = !sh.ks.wsplit && !vt && groups <= cu_count() ? 2 : 1;
+}
+
 int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor *v,
                 const cvattn_tensor *mask, SinglePlan *pl, bool vt = false) {
     int rc = check_fa(q, k, v, mask, &pl->sh, vt);
     if (rc) return rc;
+    choose_kh(pl->sh, split_work(pl->sh), vt);
     const FaShape &sh = pl->sh;
     plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len);
     pl->ws_bytes = pl->n_splits > 1 ? (size_t)slots_per_split(sh) * pl->n_splits * PART_STRIDE * sizeof(float) : 0;
@@ -390,11 +400,13 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         work += split_work(sh);
     }
     if (table) table->resize(n);
+    choose_kh(*sh0, work, false);
     int64_t unit = 0, part = 0, row = 0, cnt = 0;
     for (int i = 0; i < n; i++) {
         const cvattn_fa_problem &p = probs[i];
         FaShape sh;
         check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
+        sh.ks.kh = sh0->ks.kh;
         int ns, sl;
         plan_splits(sh, sh.n_kv, work, &ns, &sl);
         FaProblem fp;

@@ -15,6 +15,8 @@ struct FaKernelShape {
     int tstep;          // tokens per staged tile (per wave step for the decode kernel)
     int rows_per_group; // query rows per workgroup
     int max_splits;     // most token splits one workgroup can merge in-kernel
+    int kh;             // row-tiled: key halves per workgroup (1, or 2 for launches with fewer row
+                        // groups than CUs: 8 waves, two per row set, 128-token steps)
 };
 FaKernelShape fa_shape(int n_rows, bool small_views);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,

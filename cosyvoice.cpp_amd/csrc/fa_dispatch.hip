@@ -7,6 +7,7 @@ static FaLaunchFn fa_pick_decode(int mask, int batch, int ki, int vi) {
     return mask ? fa_pick_decode_m1(batch, ki, vi) : fa_pick_decode_m0(batch, ki, vi);
 }
 FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
+FaLaunchFn fa_pick_rows_kh2(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_vt(int mask, int ki, int vti);
 
 static int type_index(int t) {
@@ -32,6 +33,7 @@ FaKernelShape fa_shape(int n_rows, bool small_views) {
     s.tstep = s.wsplit ? 32 : ROWS_TS;
     s.rows_per_group = s.wsplit ? 16 : ROWS_ROWS;
     s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : ROWS_MERGE_MAX_SPLITS;
+    s.kh = 1;
     return s;
 }
 
@@ -39,7 +41,9 @@ hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bo
                      hipStream_t st) {
     const int ki = type_index(ktype), vi = type_index(vtype);
     if (ki < 0 || vi < 0) return hipErrorInvalidValue;
-    const FaLaunchFn fn = s.wsplit ? fa_pick_decode(mask, batch, ki, vi) : fa_pick_rows(mask, batch, ki, vi);
+    const FaLaunchFn fn = s.wsplit    ? fa_pick_decode(mask, batch, ki, vi)
+                          : s.kh == 2 ? fa_pick_rows_kh2(mask, batch, ki, vi)
+                                      : fa_pick_rows(mask, batch, ki, vi);
     return fn(a, st);
 }
 

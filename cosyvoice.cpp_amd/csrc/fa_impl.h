@@ -177,14 +177,20 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
     }
 }
 
-template <int KT, int VT, bool MASK, bool BATCH>
-__global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
+// KH = 2: two key halves.  The workgroup is 8 waves; waves w and w+4 own the same 16 rows and
+// take the first and second 64 tokens of each 128-token staged step, then merge through LDS.  For
+// launches with fewer row groups than CUs (prefill), where one wave per SIMD walks the whole key
+// range, this halves the chain each wave runs.
+template <int KT, int VT, bool MASK, bool BATCH, int KH>
+__global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
+    constexpr int TSS = TS * KH; // tokens per staged step
     constexpr int RSK = ROWS_RS, RSV = is_vt(VT) ? ROWS_RS_VT : ROWS_RS;
+    static_assert(KH == 1 || (KH == 2 && !is_vt(VT)), "the transposed-V tile holds one 64-token step");
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
-    __shared__ __attribute__((aligned(16))) _Float16 sK[2][TS * RSK];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TS * RSV];
-    __shared__ __attribute__((aligned(16))) float sS[2][4][2][TS]; // {kd, km, vd, vm} x block x token
+    __shared__ __attribute__((aligned(16))) _Float16 sK[2][TSS * RSK];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TSS * RSV];
+    __shared__ __attribute__((aligned(16))) float sS[2][4][2][TSS]; // {kd, km, vd, vm} x block x token
 
     const FaUniform &U = args.u;
     FaProblem P;
@@ -195,23 +201,26 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15; // MFMA column (query row) / A-operand row (token or dim)
     const int g = lane >> 4;   // lane group: k-slots 8g..8g+7, C rows 4g..4g+3
+    const int rw = wv & (ROWS_NW - 1);  // row wave: rows rw*16*NR.. of the row group
+    const int hk = KH == 2 ? wv >> 2 : 0; // key half (uniform per wave)
 
     const int t_begin = split * P.split_len;
     const int t_end = min(P.n_kv, t_begin + P.split_len);
-    const int nsteps = (max(0, t_end - t_begin) + TS - 1) / TS; // uniform
+    const int nsteps = (max(0, t_end - t_begin) + TSS - 1) / TSS; // staged steps, uniform
 
-    // ---- staging role: waves 0-1 stage K blocks, waves 2-3 V blocks; thread = (token, block) ----
+    // ---- staging role: waves 0..2KH-1 stage K blocks, the others V blocks; thread = (token, block) ----
     // Transposed V (non-flash-attention layout): thread = (dim, 16-byte run of tokens), VNCH runs
     // VDSTEP dims apart; the tile is kept dim-major in LDS, which is already the V^T operand.
     constexpr bool VTR = is_vt(VT);
     constexpr int VES = VT == T_VT_F32 ? 4 : 2;  // bytes per transposed-V element
     constexpr int VCH = 16 / VES;                 // tokens per 16-byte run
-    constexpr int VCPD = TS / VCH;                // runs per dim of a tile
-    constexpr int VDSTEP = 128 / VCPD;            // dims between one thread's runs
+    constexpr int VCPD = TSS / VCH;               // runs per dim of a tile
+    constexpr int VDSTEP = 128 * KH / VCPD;       // dims between one thread's runs
     constexpr int VNCH = HEAD / VDSTEP;           // runs per staging thread
-    const bool stage_k = wv < 2; // uniform per wave
-    const int st_tok = (tid & 127) >> 1, st_b = tid & 1;
-    const int vt_tc = (tid & 127) % VCPD, vt_d0 = (tid & 127) / VCPD;
+    const bool stage_k = wv < 2 * KH; // uniform per wave
+    const int st_idx = tid & (128 * KH - 1);
+    const int st_tok = st_idx >> 1, st_b = tid & 1;
+    const int vt_tc = st_idx % VCPD, vt_d0 = st_idx / VCPD;
     gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
     gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
     const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
@@ -254,14 +263,14 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
         }
     };
     if (nsteps > 0) load_tile(t_begin, R0);
-    if (nsteps > 1) load_tile(t_begin + TS, R1);
+    if (nsteps > 1) load_tile(t_begin + TSS, R1);
 
     // ---- this lane's query rows (one per 16-row set) and their Q operands ----
     int row[NR], iq[NR], hq[NR];
     bool row_ok[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-        row[r] = rg * ROWS_ROWS + wv * (16 * NR) + 16 * r + col;
+        row[r] = rg * ROWS_ROWS + rw * (16 * NR) + 16 * r + col;
         row_ok[r] = row[r] < U.n_rows;
         iq[r] = row_ok[r] ? row[r] / U.G : 0;
         hq[r] = kh * U.G + (row_ok[r] ? row[r] % U.G : 0);
@@ -337,7 +346,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 _Float16 *dst = sV[buf] + (vt_d0 + VDSTEP * i) * RSV + VCH * vt_tc;
                 if constexpr (VT == T_VT_F16) {
                     u4 w = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
-                    if (t0 + TS > P.n_kv) { // uniform: the cache's last tile
+                    if (t0 + TSS > P.n_kv) { // uniform: the cache's last tile
 #pragma unroll
                         for (int j = 0; j < 4; j++)
                             w[j] &= (2 * j < nvalid ? 0xffffu : 0u) | (2 * j + 1 < nvalid ? 0xffff0000u : 0u);
@@ -378,10 +387,11 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
 
     // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS) for both row sets; `full_c`
     // (std::true_type) says every token of the tile is in range, so no bounds code is emitted
+    // (t0: this wave's 64 tokens, key half hk of the staged step)
     auto compute_tile = [&](int buf, int t0, auto full_c) {
-        const _Float16 *cK = sK[buf];
-        const _Float16 *cV = sV[buf];
-        float(*cS)[2][TS] = sS[buf];
+        const _Float16 *cK = sK[buf] + hk * TS * RSK;
+        const _Float16 *cV = sV[buf] + hk * TS * RSV;
+        auto cS = [&](int x, int b) { return &sS[buf][x][b][hk * TS]; };
         constexpr bool full = decltype(full_c)::value;
         // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
         // causal prefill) contributes nothing; the wave skips it
@@ -436,12 +446,12 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                             acc0 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a0, qlo[r][0], acc0, 0, 0, 0);
                             acc1 = __builtin_amdgcn_mfma_f32_16x16x32_f16(a1, qlo[r][1], acc1, 0, 0, 0);
                         }
-                        const f4 d0 = *(const f4 *)&cS[0][0][16 * tt + 4 * g];
-                        const f4 d1 = *(const f4 *)&cS[0][1][16 * tt + 4 * g];
+                        const f4 d0 = *(const f4 *)&cS(0, 0)[16 * tt + 4 * g];
+                        const f4 d1 = *(const f4 *)&cS(0, 1)[16 * tt + 4 * g];
                         f4 v = d0 * acc0 + d1 * acc1;
                         if constexpr (has_min(KT)) {
-                            const f4 m0 = *(const f4 *)&cS[1][0][16 * tt + 4 * g];
-                            const f4 m1 = *(const f4 *)&cS[1][1][16 * tt + 4 * g];
+                            const f4 m0 = *(const f4 *)&cS(1, 0)[16 * tt + 4 * g];
+                            const f4 m1 = *(const f4 *)&cS(1, 1)[16 * tt + 4 * g];
                             v += m0 * qsum[r][0] + m1 * qsum[r][1];
                         }
                         s[r][tt] = v;
@@ -518,8 +528,8 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 for (int b = 0; b < 2; b++) {
                     f4 xlo = plo, xhi = phi;
                     if constexpr (is_quant(VT)) {
-                        xlo = plo * *(const f4 *)&cS[2][b][32 * kb + 4 * g];
-                        xhi = phi * *(const f4 *)&cS[2][b][32 * kb + 16 + 4 * g];
+                        xlo = plo * *(const f4 *)&cS(2, b)[32 * kb + 4 * g];
+                        xhi = phi * *(const f4 *)&cS(2, b)[32 * kb + 16 + 4 * g];
                     }
 #pragma unroll
                     for (int j = 0; j < 4; j++) {
@@ -527,8 +537,8 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                         pb[r][kb][b][4 + j] = (_Float16)xhi[j];
                     }
                     if constexpr (has_min(VT)) {
-                        const f4 mlo = *(const f4 *)&cS[3][b][32 * kb + 4 * g];
-                        const f4 mhi = *(const f4 *)&cS[3][b][32 * kb + 16 + 4 * g];
+                        const f4 mlo = *(const f4 *)&cS(3, b)[32 * kb + 4 * g];
+                        const f4 mhi = *(const f4 *)&cS(3, b)[32 * kb + 16 + 4 * g];
                         const f4 t = plo * mlo + phi * mhi;
                         corr[r][b] += t[0] + t[1] + t[2] + t[3];
                     }
@@ -577,30 +587,83 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
     //      from registers loaded two steps earlier ----
     if (nsteps > 0) {
         write_tile(R0, 0, t_begin);
-        if (nsteps > 2) load_tile(t_begin + 2 * TS, R0);
+        if (nsteps > 2) load_tile(t_begin + 2 * TSS, R0);
     }
     __syncthreads();
-    // full tiles run in the loop; only the last tile can be partial, and it runs after the loop
+    // full steps run in the loop; only the last step can be partial, and it runs after the loop
     // from the buffer the loop staged it into
-    const int nfull = max(0, t_end - t_begin) / TS; // uniform
+    const int nfull = max(0, t_end - t_begin) / TSS; // uniform
+    const int t_half = hk * TS;                      // this wave's tokens within a step
     for (int s0 = 0; s0 < nfull; s0 += 2) {
-        // even step: compute buffer 0, stage tile s0+1 (R1) into buffer 1
-        compute_tile(0, t_begin + s0 * TS, std::true_type{});
+        // even step: compute buffer 0, stage step s0+1 (R1) into buffer 1
+        compute_tile(0, t_begin + s0 * TSS + t_half, std::true_type{});
         if (s0 + 1 < nsteps) {
-            write_tile(R1, 1, t_begin + (s0 + 1) * TS);
-            if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TS, R1);
+            write_tile(R1, 1, t_begin + (s0 + 1) * TSS);
+            if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TSS, R1);
         }
         __syncthreads();
         if (s0 + 1 >= nfull) break;
-        // odd step: compute buffer 1, stage tile s0+2 (R0) into buffer 0
-        compute_tile(1, t_begin + (s0 + 1) * TS, std::true_type{});
+        // odd step: compute buffer 1, stage step s0+2 (R0) into buffer 0
+        compute_tile(1, t_begin + (s0 + 1) * TSS + t_half, std::true_type{});
         if (s0 + 2 < nsteps) {
-            write_tile(R0, 0, t_begin + (s0 + 2) * TS);
-            if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TS, R0);
+            write_tile(R0, 0, t_begin + (s0 + 2) * TSS);
+            if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TSS, R0);
         }
         __syncthreads();
     }
-    if (nfull < nsteps) compute_tile(nfull & 1, t_begin + nfull * TS, std::false_type{});
+    if (nfull < nsteps) {
+        // the partial last step: with two key halves, a half's 64 tokens may be full, partial or
+        // past the end (uniform per wave)
+        const int t0w = t_begin + nfull * TSS + t_half;
+        if constexpr (KH == 1) {
+            compute_tile(nfull & 1, t0w, std::false_type{});
+        } else {
+            if (t0w + TS <= t_end) compute_tile(nfull & 1, t0w, std::true_type{});
+            else if (t0w < t_end) compute_tile(nfull & 1, t0w, std::false_type{});
+        }
+    }
+
+    // two key halves: half 1 hands (m, l, corr, O) of each lane to the same lane of half 0, which
+    // merges them (O and l scale by 2^(m - max), as in a split merge); half 0 alone stores
+    const bool writer = KH == 1 || hk == 0; // uniform per wave
+    if constexpr (KH == 2) {
+        constexpr int XV = 4 + 16;                // values per lane and row set
+        float *xch = (float *)&sK[0][0];          // 4 row waves x NR x XV x 64 lanes
+        __syncthreads();                          // every wave is done with the K/V tiles
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            float *x = xch + ((rw * NR + r) * XV) * 64 + lane;
+            if (hk == 1) {
+                x[0] = m_ref[r];
+                x[64] = l_run[r];
+                x[128] = corr[r][0];
+                x[192] = corr[r][1];
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) x[(4 + 4 * i + j) * 64] = oacc[r][i][j];
+            }
+        }
+        __syncthreads();
+        if (hk == 0) {
+#pragma unroll
+            for (int r = 0; r < NR; r++) {
+                const float *x = xch + ((rw * NR + r) * XV) * 64 + lane;
+                const float m1 = x[0];
+                const float M = fmaxf(m_ref[r], m1);
+                const float w0 = M == -INFINITY ? 0.0f : fast_exp2(m_ref[r] - M);
+                const float w1 = M == -INFINITY ? 0.0f : fast_exp2(m1 - M);
+                l_run[r] = l_run[r] * w0 + x[64] * w1;
+                corr[r][0] = corr[r][0] * w0 + x[128] * w1;
+                corr[r][1] = corr[r][1] * w0 + x[192] * w1;
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+#pragma unroll
+                    for (int j = 0; j < 4; j++) oacc[r][i][j] = oacc[r][i][j] * w0 + x[(4 + 4 * i + j) * 64] * w1;
+                m_ref[r] = M;
+            }
+        }
+    }
 
     // ---------------- epilogue ----------------
     // partial slot of (row r of this row group, split s) = slot0 + r * n_splits + s
@@ -614,7 +677,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
 #pragma unroll
             for (int i = 0; i < 4; i++) oacc[r][i] += corr[r][i >> 1];
         }
-        if (row_ok[r]) {
+        if (writer && row_ok[r]) {
             if (P.n_splits == 1) {
                 // a row with every key masked: 0 (flash attention) or NaN (soft_max path)
                 const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : U.empty_row;
@@ -660,7 +723,7 @@ __global__ __launch_bounds__(64 * ROWS_NW) void fa_rows_kernel(FaArgs args) {
                 s_last = last ? 1u : 0u;
             }
             __syncthreads();
-            if (s_last) merge_splits<ROWS_ROWS, 64 * ROWS_NW>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
+            if (s_last) merge_splits<ROWS_ROWS, 64 * ROWS_NW * KH>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
         }
     }
 }
@@ -706,11 +769,11 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
 
 using FaLaunchFn = hipError_t (*)(const FaArgs &, hipStream_t);
 
-template <int KT, int VT, bool MASK, bool BATCH>
+template <int KT, int VT, bool MASK, bool BATCH, int KH = 1>
 hipError_t launch_rows(const FaArgs &a, hipStream_t st) {
     if (a.u.total_units <= 0) return hipSuccess;
-    hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH>), dim3((unsigned)a.u.total_units), dim3(64 * ROWS_NW), 0,
-                       st, a);
+    hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH, KH>), dim3((unsigned)a.u.total_units),
+                       dim3(64 * ROWS_NW * KH), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // single calls merge split partials with a second launch; prepared batches merge in-kernel
@@ -722,15 +785,15 @@ hipError_t launch_rows(const FaArgs &a, hipStream_t st) {
 }
 
 // Launch table [k type index][v type index]; index order f32 f16 q8_0 q4_0 q4_1 q5_0 q5_1.
-#define CVATTN_V_ROW(KT, MASK, BATCH)                                                                \
-    {launch_rows<KT, T_F32, MASK, BATCH>, launch_rows<KT, T_F16, MASK, BATCH>,                     \
-     launch_rows<KT, T_Q8_0, MASK, BATCH>, launch_rows<KT, T_Q4_0, MASK, BATCH>,                   \
-     launch_rows<KT, T_Q4_1, MASK, BATCH>, launch_rows<KT, T_Q5_0, MASK, BATCH>,                   \
-     launch_rows<KT, T_Q5_1, MASK, BATCH>}
-#define CVATTN_TABLE(MASK, BATCH)                                                                     \
-    {CVATTN_V_ROW(T_F32, MASK, BATCH), CVATTN_V_ROW(T_F16, MASK, BATCH),                           \
-     CVATTN_V_ROW(T_Q8_0, MASK, BATCH), CVATTN_V_ROW(T_Q4_0, MASK, BATCH),                         \
-     CVATTN_V_ROW(T_Q4_1, MASK, BATCH), CVATTN_V_ROW(T_Q5_0, MASK, BATCH),                         \
-     CVATTN_V_ROW(T_Q5_1, MASK, BATCH)}
+#define CVATTN_V_ROW(KT, MASK, BATCH, KH)                                                            \
+    {launch_rows<KT, T_F32, MASK, BATCH, KH>, launch_rows<KT, T_F16, MASK, BATCH, KH>,             \
+     launch_rows<KT, T_Q8_0, MASK, BATCH, KH>, launch_rows<KT, T_Q4_0, MASK, BATCH, KH>,           \
+     launch_rows<KT, T_Q4_1, MASK, BATCH, KH>, launch_rows<KT, T_Q5_0, MASK, BATCH, KH>,           \
+     launch_rows<KT, T_Q5_1, MASK, BATCH, KH>}
+#define CVATTN_TABLE(MASK, BATCH, KH)                                                                 \
+    {CVATTN_V_ROW(T_F32, MASK, BATCH, KH), CVATTN_V_ROW(T_F16, MASK, BATCH, KH),                   \
+     CVATTN_V_ROW(T_Q8_0, MASK, BATCH, KH), CVATTN_V_ROW(T_Q4_0, MASK, BATCH, KH),                 \
+     CVATTN_V_ROW(T_Q4_1, MASK, BATCH, KH), CVATTN_V_ROW(T_Q5_0, MASK, BATCH, KH),                 \
+     CVATTN_V_ROW(T_Q5_1, MASK, BATCH, KH)}
 
 } // namespace cvattn
