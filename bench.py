@@ -303,6 +303,34 @@ def read_traffic():
     return None
 
 
+def stream_floor(torch, dev):
+    """What plain streaming kernels reach over a working set the size of one decode step
+    (20,619,264 B), cycled over 27 buffers so the 256 MB last-level cache cannot hold it, and over
+    4x and 16x that size: torch's device copy (read + write) and a sum (read)."""
+    step = 20619264
+    out = []
+    for mult, n_buf in ((1, 27), (4, 4), (16, 4)):
+        nbytes = step * mult
+        bufs = [torch.randn(nbytes // 4, device=dev) for _ in range(n_buf)]
+        dst = [torch.empty_like(bufs[0]) for _ in range(2)]
+        red = torch.empty((), device=dev)
+
+        def launch_copy(s):
+            for i, b in enumerate(bufs):
+                dst[i & 1].copy_(b)
+
+        def launch_sum(s):
+            for b in bufs:
+                torch.sum(b, dim=0, out=red)
+
+        for name, fn, moved in (("copy", launch_copy, 2 * nbytes), ("sum", launch_sum, nbytes)):
+            ms, _ = time_graph(torch, fn, n_buf, 10 * n_buf, n_buf)
+            out.append({"kernel": name, "working_set_bytes": nbytes, "us": ms * 1e3,
+                        "gbs_moved": moved / (ms * 1e-3) / 1e9})
+        del bufs, dst
+    return {"stream_floor": out}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,6 +341,9 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill, DiT-stream and serving legs")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 256 MiB device copies (reference kernels for the HBM counters)")
+    ap.add_argument("--stream-floor", action="store_true",
+                    help="only time plain device copies and sums over the decode step's 20.6 MB working set "
+                         "(27 copies cycled, as the decode leg), and over 4x and 16x that size")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the attention path runs "
@@ -336,6 +367,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
                           "launches": {"copyBuffer": 10, "neg": 10}}))
+        return
+    if args.stream_floor:
+        print(json.dumps(stream_floor(torch, dev)))
         return
     lib = cvattn.lib()
     kt, vt = cvattn.Q8_0, cvattn.Q4_0
