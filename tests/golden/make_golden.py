@@ -44,7 +44,7 @@ def block_fixture(orc):
     np.savez_compressed(os.path.join(OUT, "blocks.npz"), **data)
 
 
-def attn_cfg1(orc):
+def attn_decode_512_f16(orc):
     """Single-layer Qwen2-0.5B decode: 14/2 heads, D=64, f16 KV, n_kv=512, scale 1/8, no mask."""
     rng = np.random.default_rng(1)
     H, Hkv, D, nkv = 14, 2, 64, 512
@@ -58,7 +58,7 @@ def attn_cfg1(orc):
     kt = view(kh, F16, [D, nkv, Hkv, 1], [2, row, row // Hkv, row * nkv])
     vt = view(vh, F16, [D, nkv, Hkv, 1], [2, row, row // Hkv, row * nkv])
     out = orc.fa_f64(qt, kt, vt, None, 0.125, (1, 1, H, D))
-    np.savez_compressed(os.path.join(OUT, "attn_cfg1.npz"), q=q, k_f16=kh, v_f16=vh, out=out.reshape(H, D))
+    np.savez_compressed(os.path.join(OUT, "attn_decode_512_f16.npz"), q=q, k_f16=kh, v_f16=vh, out=out.reshape(H, D))
 
 
 def attn_prefill_small(orc):
@@ -102,7 +102,7 @@ def attn_dit_small(orc):
 def main():
     orc = oracle()
     block_fixture(orc)
-    attn_cfg1(orc)
+    attn_decode_512_f16(orc)
     attn_prefill_small(orc)
     attn_dit_small(orc)
     print("wrote fixtures to", OUT)

@@ -77,9 +77,9 @@ def run_case(eng, orc, c, scale=0.125, what=""):
 # ------------------------------------------------------------------------------------------
 # committed fixtures
 # ------------------------------------------------------------------------------------------
-def test_golden_cfg1_decode_f16(eng, cuda):
-    """Config 1: single-layer decode, 14/2 heads, f16 KV, n_kv 512, scale 1/8, no mask."""
-    g = np.load(os.path.join(GOLDEN, "attn_cfg1.npz"))
+def test_golden_decode_512_f16(eng, cuda):
+    """Single-layer Qwen2 decode: 14/2 heads, f16 KV, n_kv 512, scale 1/8, no mask."""
+    g = np.load(os.path.join(GOLDEN, "attn_decode_512_f16.npz"))
     q, kh, vh = g["q"], g["k_f16"], g["v_f16"]
     dq, dk, dv = dev(q), dev(kh), dev(vh)
     qd = cvattn.llm_q_view(dq.data_ptr(), D, 14, 1)
@@ -87,7 +87,7 @@ def test_golden_cfg1_decode_f16(eng, cuda):
     vd = cvattn.llm_kv_view(dv.data_ptr(), F16, D, 2, 512, 512)
     out = empty_f32(14, D)
     run_fa(eng, qd, kd, vd, None, cvattn.out_view(out.data_ptr(), D, 14, 1))
-    check_close(host(out), g["out"], what="cfg1")
+    check_close(host(out), g["out"], what="decode 512 f16 fixture")
 
 
 def test_golden_prefill_small(eng, cuda):
@@ -128,8 +128,8 @@ def test_decode_type_pairs(eng, orc, rng, kt, vt, cuda):
 
 
 @pytest.mark.parametrize("kt,vt", [(Q8_0, Q4_0), (Q8_0, Q8_0), (F16, F16), (Q5_1, Q5_1)])
-def test_decode_config2_layer(eng, orc, rng, kt, vt, cuda):
-    """Config 2 layer shape: n_kv 4096 in a 4096-row cache, 14/2 heads (split over the chip)."""
+def test_decode_4096_token_layer(eng, orc, rng, kt, vt, cuda):
+    """One Qwen2 layer over a full 4096-row cache (n_kv 4096), 14/2 heads (split over the chip)."""
     c = llm_case(orc, rng, nq=1, nkv=4096, kt=kt, vt=vt, max_seq=4096)
     run_case(eng, orc, c, what="cfg2 layer")
 
@@ -355,19 +355,19 @@ def run_batch(eng, cases, masked=False):
     return ws
 
 
-def test_config2_24_layer_step(eng, orc, cuda):
-    """Config 2 as the benchmark runs it: 24 layers x 4096 cached tokens, K q8_0 / V q4_0, one
+def test_decode_24_layer_4096_token_step(eng, orc, cuda):
+    """The decode step as the benchmark runs it: 24 layers x 4096 cached tokens, K q8_0 / V q4_0, one
     prepared batch (one launch with in-kernel split merges), every layer against the oracle."""
     rng = np.random.default_rng(2026)
     cases = [llm_case(orc, rng, nq=1, nkv=4096, kt=Q8_0, vt=Q4_0, max_seq=4096) for _ in range(24)]
     run_batch(eng, cases)
     for i, c in enumerate(cases):
         want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
-        check_close(host(c.dst), want, what=f"config 2 layer {i}")
+        check_close(host(c.dst), want, what=f"24-layer step, layer {i}")
 
 
-def test_config3_serving_batch(eng, orc, cuda):
-    """Config 3: 16 sequences with kv_len drawn from U{256..8192} (the benchmark's seed), q8_0 K and
+def test_serving_16_ragged_sequences(eng, orc, cuda):
+    """Serving decode: 16 sequences with kv_len drawn from U{256..8192} (the benchmark's seed), q8_0 K and
     V, one layer's 16 problems in one launch."""
     lens = np.random.default_rng(20261201).integers(256, 8193, 16)
     rng = np.random.default_rng(33)
@@ -375,13 +375,13 @@ def test_config3_serving_batch(eng, orc, cuda):
     run_batch(eng, cases)
     for c, n in zip(cases, lens):
         want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
-        check_close(host(c.dst), want, what=f"config 3 kv_len {n}")
+        check_close(host(c.dst), want, what=f"serving kv_len {n}")
 
 
-def test_config4_prefill_1024_causal(eng, orc, cuda):
-    """Config 4: 1024 query tokens over 1024 f16 cached tokens with the causal mask, Q/K/V scaled
+def test_prefill_1024_causal(eng, orc, cuda):
+    """LLM prefill: 1024 query tokens over 1024 f16 cached tokens with the causal mask, Q/K/V scaled
     by 0.5 (src/cosyvoice-llm.cpp:20-29,101-108)."""
     rng = np.random.default_rng(44)
     mask = orc.causal_mask(1024, 1024)
     c = llm_case(orc, rng, nq=1024, nkv=1024, kt=F16, vt=F16, max_seq=1024, mask=mask, qscale=0.5, kvscale=0.5)
-    run_case(eng, orc, c, what="config 4 prefill")
+    run_case(eng, orc, c, what="1024-token causal prefill")
