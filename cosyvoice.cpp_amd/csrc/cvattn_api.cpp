@@ -18,7 +18,8 @@ using namespace cvattn;
 
 namespace {
 
-constexpr int kRowsPerCu = 3; // resident row-tiled workgroups per CU (register bound)
+constexpr int kRowsPerCu = 3;   // resident row-tiled workgroups per CU (register bound)
+constexpr int kDecodePerCu = 3; // resident decode workgroups per CU (41 KB of LDS each)
 
 // Compute units of the current device (256 on MI355X), cached per device.
 int cu_count() {
@@ -138,7 +139,9 @@ constexpr int64_t kTargetWaves = 4096;
 // row-tiled kernel cost terms (MI355X, measured): one 64-token tile of a workgroup, and the fixed
 // cost of a split (partial stores, arrival counter, last-arrival merge)
 constexpr double kTileUs = 0.85, kMergeUs = 3.4;
-void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len) {
+// two_rounds: the decode kernel may merge up to two rounds of splits (long sequences); the
+// callers turn it off when the extra splits would not all be resident at once.
+void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *split_len, bool two_rounds = true) {
     // row-tiled with two key halves: 128-token steps
     const int tstep = sh.ks.wsplit ? sh.ks.tstep : sh.ks.tstep * sh.ks.kh;
     int len;
@@ -175,8 +178,12 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         len = std::max(tstep, (len + tstep - 1) / tstep * tstep);
     }
     const int unit = sh.ks.wsplit ? tstep * sh.ks.nw : tstep;
-    // never more splits than the in-kernel merge takes in one pass
-    const int max_splits = sh.ks.max_splits;
+    // never more splits than the in-kernel merge takes; the decode kernel's second merge round
+    // is used only for sequences that one round's splits would leave long per workgroup
+    int max_splits = sh.ks.max_splits;
+    if (sh.ks.wsplit &&
+        (!two_rounds || (n_kv + sh.ks.round_splits - 1) / sh.ks.round_splits <= sh.ks.long_split))
+        max_splits = sh.ks.round_splits;
     const int min_len = (n_kv + max_splits - 1) / max_splits;
     if (len < min_len) len = (min_len + unit - 1) / unit * unit;
     *split_len = len;
@@ -267,6 +274,8 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
     choose_kh(pl->sh, split_work(pl->sh), vt);
     const FaShape &sh = pl->sh;
     plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len);
+    if (sh.ks.wsplit && (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * pl->n_splits > kDecodePerCu * cu_count())
+        plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len, false);
     pl->ws_bytes = pl->n_splits > 1 ? (size_t)slots_per_split(sh) * pl->n_splits * PART_STRIDE * sizeof(float) : 0;
     return CVATTN_OK;
 }
@@ -401,6 +410,20 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
     }
     if (table) table->resize(n);
     choose_kh(*sh0, work, false);
+    // decode: a second merge round only if all workgroups of the launch stay resident
+    bool two_rounds = true;
+    if (sh0->ks.wsplit) {
+        int64_t units = 0;
+        for (int i = 0; i < n; i++) {
+            const cvattn_fa_problem &p = probs[i];
+            FaShape sh;
+            check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
+            int ns, sl;
+            plan_splits(sh, sh.n_kv, work, &ns, &sl);
+            units += (int64_t)sh.B * sh.H_kv * sh.n_rowgroups * ns;
+        }
+        two_rounds = units <= kDecodePerCu * cu_count();
+    }
     int64_t unit = 0, part = 0, row = 0, cnt = 0;
     for (int i = 0; i < n; i++) {
         const cvattn_fa_problem &p = probs[i];
@@ -408,7 +431,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
         sh.ks.kh = sh0->ks.kh;
         int ns, sl;
-        plan_splits(sh, sh.n_kv, work, &ns, &sl);
+        plan_splits(sh, sh.n_kv, work, &ns, &sl, two_rounds);
         FaProblem fp;
         fill_problem(fp, &p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &p.dst, sh);
         fp.n_splits = ns;

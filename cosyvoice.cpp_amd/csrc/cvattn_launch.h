@@ -15,6 +15,8 @@ struct FaKernelShape {
     int tstep;          // tokens per staged tile (per wave step for the decode kernel)
     int rows_per_group; // query rows per workgroup
     int max_splits;     // most token splits one workgroup can merge in-kernel
+    int round_splits;   // decode: splits per merge round; a second round only when one round's
+    int long_split;     //   splits would leave a workgroup more than long_split tokens
     int kh;             // row-tiled: key halves per workgroup (1, or 2 for launches with fewer row
                         // groups than CUs: 8 waves, two per row set, 128-token steps)
 };

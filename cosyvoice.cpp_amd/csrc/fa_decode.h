@@ -32,10 +32,14 @@ namespace cvattn {
 constexpr int DEC_NW = 4;      // waves per workgroup
 constexpr int DEC_RS = 72;     // halfs per canonical LDS row (64 dims + pad): 144 B
 constexpr float DEC_RESCALE_LOG2 = 8.0f;
-// Most token splits per group, merged in one pass by the last-arriving workgroup.  The merge's
-// loads are issued by one CU, and past 16 splits it costs more than the streaming it shortens
-// (the 24-layer 4096-token q8_0/q4_0 step and the one-layer launch both measured best at 16).
+// Token splits per merge round of the last-arriving workgroup: all loads of a round are issued
+// at once.  Past 16 splits a second round costs more than the streaming it shortens for 4096-token
+// sequences (the 24-layer q8_0/q4_0 step and the one-layer launch both measured best at 16), so
+// the planner goes to two rounds (DEC_MAX_SPLITS) only for sequences long enough that 16 splits
+// would leave a workgroup more than DEC_LONG_SPLIT tokens.
 constexpr int DEC_MERGE_CHUNK = 16;
+constexpr int DEC_MAX_SPLITS = 2 * DEC_MERGE_CHUNK;
+constexpr int DEC_LONG_SPLIT = 256;
 
 // Steps whose raw blocks are in flight at once (register budget per type pair).
 template <int KT, int VT>
@@ -59,10 +63,11 @@ __device__ __forceinline__ bool dec_row(const FaUniform &U, int kh, int rg, int 
 __device__ __forceinline__ int dec_ml_offset(int ns) { return 16 * ns * 64; }
 __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 
-// Merge the ns (<= DEC_MERGE_CHUNK) split partials of one group's 16 row slots into dst; thread =
-// (slot, 4 dims).  Every load is issued before any is used, and every lane of a row loads all of
-// the row's (m, l) pairs (the same bytes for the row's 16 lanes), so the weights need no
-// cross-lane exchange: one round trip to memory, then VALU only.
+// Merge the ns (<= DEC_MAX_SPLITS) split partials of one group's 16 row slots into dst; thread =
+// (slot, 4 dims).  Splits are merged in rounds of DEC_MERGE_CHUNK: every load of a round is
+// issued before any is used, and every lane of a row loads all of the round's (m, l) pairs of the
+// row (the same bytes for the row's 16 lanes), so the weights need no cross-lane exchange.  A
+// second round rescales the running sum to the new maximum.
 // SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
 template <bool SC1>
 __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int kh,
@@ -78,32 +83,41 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
     // Loads of row slots past the group's rows (never written) and of splits past ns point
     // outside the resource: they return 0 without a memory access, and need no branch.
     constexpr int kOutside = 0x7ffffff0;
-    u4 ov[DEC_MERGE_CHUNK];
-    u4 ml[DEC_MERGE_CHUNK / 2]; // (m, l) of splits 2j and 2j+1
-#pragma unroll
-    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        ov[j] = __builtin_amdgcn_raw_buffer_load_b128(rp, ok && j < ns ? ((r * ns + j) * 64 + d0) * 4 : kOutside, 0,
-                                                      AUX);
-#pragma unroll
-    for (int j = 0; j < DEC_MERGE_CHUNK / 2; j++)
-        ml[j] = __builtin_amdgcn_raw_buffer_load_b128(
-            rp, ok && 2 * j < ns ? (dec_ml_offset(ns) + (r * nsp + 2 * j) * 2) * 4 : kOutside, 0, AUX);
-    if (!ok) return;
-    float M = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        if (j < ns) M = fmaxf(M, as_f32(ml[j >> 1][2 * (j & 1)]));
-    const float Mu = M == -INFINITY ? 0.0f : M;
-    float L = 0.0f;
+    float M = -INFINITY, L = 0.0f;
     f4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c0 = 0; c0 < ns; c0 += DEC_MERGE_CHUNK) { // one round, or two (uniform)
+        u4 ov[DEC_MERGE_CHUNK];
+        u4 ml[DEC_MERGE_CHUNK / 2]; // (m, l) of splits c0+2j and c0+2j+1
 #pragma unroll
-    for (int j = 0; j < DEC_MERGE_CHUNK; j++)
-        if (j < ns) {
-            const float m = as_f32(ml[j >> 1][2 * (j & 1)]);
-            const float w = m == -INFINITY ? 0.0f : fast_exp2(m - Mu);
-            L += as_f32(ml[j >> 1][2 * (j & 1) + 1]) * w;
-            acc += as_f4(ov[j]) * w;
+        for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+            ov[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                rp, ok && c0 + j < ns ? ((r * ns + c0 + j) * 64 + d0) * 4 : kOutside, 0, AUX);
+#pragma unroll
+        for (int j = 0; j < DEC_MERGE_CHUNK / 2; j++)
+            ml[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                rp, ok && c0 + 2 * j < ns ? (dec_ml_offset(ns) + (r * nsp + c0 + 2 * j) * 2) * 4 : kOutside, 0, AUX);
+        if (!ok) continue;
+        float Mc = M;
+#pragma unroll
+        for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+            if (c0 + j < ns) Mc = fmaxf(Mc, as_f32(ml[j >> 1][2 * (j & 1)]));
+        const float Mu = Mc == -INFINITY ? 0.0f : Mc;
+        if (M != -INFINITY && Mc != M) { // a later round raised the maximum: rescale what is summed
+            const float s = fast_exp2(M - Mu);
+            L *= s;
+            acc *= s;
         }
+#pragma unroll
+        for (int j = 0; j < DEC_MERGE_CHUNK; j++)
+            if (c0 + j < ns) {
+                const float m = as_f32(ml[j >> 1][2 * (j & 1)]);
+                const float w = m == -INFINITY ? 0.0f : fast_exp2(m - Mu);
+                L += as_f32(ml[j >> 1][2 * (j & 1) + 1]) * w;
+                acc += as_f4(ov[j]) * w;
+            }
+        M = Mc;
+    }
+    if (!ok) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
 }

@@ -32,7 +32,9 @@ FaKernelShape fa_shape(int n_rows, bool small_views) {
     s.nw = 4;
     s.tstep = s.wsplit ? 32 : ROWS_TS;
     s.rows_per_group = s.wsplit ? 16 : ROWS_ROWS;
-    s.max_splits = s.wsplit ? DEC_MERGE_CHUNK : ROWS_MERGE_MAX_SPLITS;
+    s.max_splits = s.wsplit ? DEC_MAX_SPLITS : ROWS_MERGE_MAX_SPLITS;
+    s.round_splits = s.wsplit ? DEC_MERGE_CHUNK : ROWS_MERGE_MAX_SPLITS;
+    s.long_split = DEC_LONG_SPLIT;
     s.kh = 1;
     return s;
 }
