@@ -9,7 +9,9 @@
 // per set.  A workgroup is 4 waves (64 rows with one set) sharing 64-token K/V tiles that are
 // staged once per step into LDS, double-buffered: while the waves compute tile s, the
 // tile s+1 is unpacked into the other buffer from registers loaded two steps ahead, so a step
-// has one barrier.
+// has one barrier.  With two key halves (KH = 2, for launches with fewer row groups than CUs) a
+// workgroup is 8 waves: a step stages 128 tokens, waves w and w+4 compute the two 64-token
+// halves for the same rows, and the halves are merged through LDS at the end.
 //
 // Per wave and 16-token tile (v_mfma_f32_16x16x32_f16, two 32-dim K halves):
 //   S^T[t][r] = K[t][:] . Q[r][:]     A = K rows from the LDS tile, B = Q^T (registers)
