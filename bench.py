@@ -175,9 +175,12 @@ def bench_prefill(lib, cvattn, torch, dev, iters=48):
     ms, n = time_graph(torch, launch, L, iters, L)
     visible = sum(nkv - nq + ii + 1 for ii in range(nq))
     flops = 4.0 * D * H * visible
+    # stored bytes per call: Q f32, K and V f16, O f32, the f16 mask
+    nbytes = nq * H * D * 4 + 2 * nkv * HKV * D * 2 + nq * H * D * 4 + nq * nkv * 2
     return {"workload": "LLM prefill layer call, 1024 query tokens, causal mask, 1024 f16 cached tokens, 14/2 heads",
             "us_per_layer_call": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12,
-            "mfma_frac": flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS}
+            "mfma_frac": flops / (ms * 1e-3) / 1e12 / FP16_DENSE_PEAK_TFLOPS,
+            "bytes_per_call": nbytes, "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
 
 
 def bench_dit_stream(lib, cvattn, torch, dev, iters=220):
@@ -284,9 +287,27 @@ def cpu_baseline(kbuf, vbuf, q, budget_s=12.0):
     sec_per_token = el / (layers_done / L)
     gbs = decode_bytes_per_layer(34, 18) * L / sec_per_token / 1e9
     return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
+            "host_cores": os.cpu_count(), "cpu_model": cpu_model(),
             "tok_per_s": 1.0 / sec_per_token,
             "sample": f"{layers_done // L} tokens x 24 layers of the same q8_0/q4_0 4096-token decode, "
                       f"ggml CPU flash-attention loop restated in C (oracle/oracle.c), {threads} threads"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def device_info(torch):
+    p = torch.cuda.get_device_properties(0)
+    return {"name": p.name, "gcn_arch": getattr(p, "gcnArchName", None), "compute_units": p.multi_processor_count,
+            "hbm_bytes": p.total_memory}
 
 
 def read_traffic():
@@ -438,6 +459,7 @@ def main():
         "vs_baseline": None,
         "dtype": "f16 MFMA + f32",
         "data": "synthetic: seeded N(0,1) K/V quantized on device with ggml's reference quantizers, N(0,1) Q",
+        "device": device_info(torch),
         "config": {
             "workload": "decode attention, 24 layers x 1 token, batch 1, 14/2 heads, head_dim 64, "
                         "kv_len 4096, K q8_0 / V q4_0 (the 24 layers run as one prepared batch)",
