@@ -378,11 +378,18 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
 
     float m_ref[NR], l_run[NR], corr[NR][2];
     f4 oacc[NR][4];
+    // unquantized V: the row sums come out of the PV MFMAs as a 65th output dim, from an A operand
+    // whose row 0 is ones (lane (col, g) holds A[col][8g..8g+7]): C[0][row] = sum_t P[t][row]
+    f4 lacc[NR];
+    h8 ones_a;
+#pragma unroll
+    for (int j = 0; j < 8; j++) ones_a[j] = col == 0 ? (_Float16)1.0f : (_Float16)0.0f;
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         m_ref[r] = -INFINITY; // reference maximum (base 2) of this lane's row
         l_run[r] = 0.0f;
         corr[r][0] = corr[r][1] = 0.0f;
+        lacc[r] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int i = 0; i < 4; i++) oacc[r][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -509,6 +516,7 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
                 corr[r][1] *= alpha;
 #pragma unroll
                 for (int i = 0; i < 4; i++) oacc[r][i] *= alpha;
+                lacc[r] *= alpha;
             }
             m_ref[r] = m_new;
             const float m_use = m_ref[r] == -INFINITY ? 0.0f : m_ref[r];
@@ -519,7 +527,7 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
                     const float p = fast_exp2(__builtin_fmaf(s[r][tt][j], sm2, -m_use));
                     s[r][tt][j] = p;
                     // with quantized V the row sum is taken here; otherwise from the fp16 weights
-                    // the PV product uses (v_dot2 over pairs, below)
+                    // the PV product uses (an extra MFMA against a ones row, below)
                     if constexpr (is_quant(VT)) l_run[r] += p;
                 }
             // P^T operands: 32 tokens (tiles 2kb and 2kb+1) per MFMA, V block scale folded in
@@ -546,11 +554,6 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
                     }
                     if constexpr (!is_quant(VT)) {
                         pb[r][kb][1] = pb[r][kb][0]; // one B operand serves both blocks
-                        const h2 one = {(_Float16)1.0f, (_Float16)1.0f};
-#pragma unroll
-                        for (int j = 0; j < 8; j += 2)
-                            l_run[r] = __builtin_amdgcn_fdot2(h2{pb[r][kb][0][j], pb[r][kb][0][j + 1]}, one,
-                                                              l_run[r], false);
                         break;
                     }
                 }
@@ -581,6 +584,11 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
 #pragma unroll
                 for (int r = 0; r < NR; r++)
                     oacc[r][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, pb[r][kb][i >> 1], oacc[r][i], 0, 0, 0);
+            }
+            if constexpr (!is_quant(VT)) {
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    lacc[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones_a, pb[r][kb][0], lacc[r], 0, 0, 0);
             }
         }
     };
@@ -623,6 +631,12 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
             if (t0w + TS <= t_end) compute_tile(nfull & 1, t0w, std::true_type{});
             else if (t0w < t_end) compute_tile(nfull & 1, t0w, std::false_type{});
         }
+    }
+
+    // unquantized V: this lane's share of the row sum (the row's lane group 0 holds it all)
+    if constexpr (!is_quant(VT)) {
+#pragma unroll
+        for (int r = 0; r < NR; r++) l_run[r] = g == 0 ? lacc[r][0] : 0.0f;
     }
 
     // two key halves: half 1 hands (m, l, corr, O) of each lane to the same lane of half 0, which
