@@ -506,19 +506,24 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
 #pragma unroll
                 for (int j = 0; j < 4; j++) mx = fmaxf(mx, s[r][tt][j]);
             }
-            mx = wave_max16x4(mx) * sm2;
-            const bool raise = mx > m_ref[r] + ROWS_RESCALE_LOG2;
-            const float m_new = raise ? mx : m_ref[r];
-            if (__builtin_amdgcn_ballot_w64(raise && m_ref[r] != -INFINITY)) { // uniform
-                const float alpha = fast_exp2(m_ref[r] - m_new);
-                l_run[r] *= alpha;
-                corr[r][0] *= alpha;
-                corr[r][1] *= alpha;
+            // A row's maximum can only clear the threshold if one of its lanes' maxima does: the
+            // cross-lane reduction and the raise run only when some lane of the wave needs it
+            // (the first tiles, then rarely), and give the same reference as running every tile
+            if (__builtin_amdgcn_ballot_w64(mx * sm2 > m_ref[r] + ROWS_RESCALE_LOG2)) { // uniform
+                mx = wave_max16x4(mx) * sm2;
+                const bool raise = mx > m_ref[r] + ROWS_RESCALE_LOG2;
+                const float m_new = raise ? mx : m_ref[r];
+                if (__builtin_amdgcn_ballot_w64(raise && m_ref[r] != -INFINITY)) { // uniform
+                    const float alpha = fast_exp2(m_ref[r] - m_new);
+                    l_run[r] *= alpha;
+                    corr[r][0] *= alpha;
+                    corr[r][1] *= alpha;
 #pragma unroll
-                for (int i = 0; i < 4; i++) oacc[r][i] *= alpha;
-                lacc[r] *= alpha;
+                    for (int i = 0; i < 4; i++) oacc[r][i] *= alpha;
+                    lacc[r] *= alpha;
+                }
+                m_ref[r] = m_new;
             }
-            m_ref[r] = m_new;
             const float m_use = m_ref[r] == -INFINITY ? 0.0f : m_ref[r];
 #pragma unroll
             for (int tt = 0; tt < NTILE; tt++)
