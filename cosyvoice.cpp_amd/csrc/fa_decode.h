@@ -319,18 +319,22 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
                     for (int j = 0; j < 4; j++) mx = fmaxf(mx, sc[s][j]);
                 }
-                mx = wave_max16x4(mx);
-                const bool raise = mx > m_ref + DEC_RESCALE_LOG2;
-                const float m_new = raise ? mx : m_ref;
-                if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
-                    const float alpha = fast_exp2(m_ref - m_new);
-                    l_run *= alpha;
-                    corr[0] *= alpha;
-                    corr[1] *= alpha;
+                // the cross-lane reduction and the raise only when some lane's maximum clears the
+                // threshold (a row's maximum can only clear it through one of its lanes)
+                if (__builtin_amdgcn_ballot_w64(mx > m_ref + DEC_RESCALE_LOG2)) { // uniform
+                    mx = wave_max16x4(mx);
+                    const bool raise = mx > m_ref + DEC_RESCALE_LOG2;
+                    const float m_new = raise ? mx : m_ref;
+                    if (__builtin_amdgcn_ballot_w64(raise && m_ref != -INFINITY)) { // uniform
+                        const float alpha = fast_exp2(m_ref - m_new);
+                        l_run *= alpha;
+                        corr[0] *= alpha;
+                        corr[1] *= alpha;
 #pragma unroll
-                    for (int i = 0; i < 4; i++) oacc[i] *= alpha;
+                        for (int i = 0; i < 4; i++) oacc[i] *= alpha;
+                    }
+                    m_ref = m_new;
                 }
-                m_ref = m_new;
                 const float m_use = m_ref == -INFINITY ? 0.0f : m_ref;
 
                 // ---- P^T operands (V block scale folded in) and O^T += V^T P^T ----
