@@ -184,15 +184,20 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 // launches with fewer row groups than CUs (prefill), where one wave per SIMD walks the whole key
 // range, this halves the chain each wave runs.
 template <int KT, int VT, bool MASK, bool BATCH, int KH>
-__global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args) {
+__global__ __launch_bounds__(64 * ROWS_NW * KH) __attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 ? 3 : 1)))
+void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int TSS = TS * KH; // tokens per staged step
     constexpr int RSK = ROWS_RS, RSV = is_vt(VT) ? ROWS_RS_VT : ROWS_RS;
     static_assert(KH == 1 || (KH == 2 && !is_vt(VT)), "the transposed-V tile holds one 64-token step");
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
+    // K tiles double-buffered, V tiles triple-buffered: the PV product of tile s runs after the
+    // barrier that ends step s, beside the QK product of tile s+1, while step s+1 stages tile s+2
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][TSS * RSK];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[2][TSS * RSV];
-    __shared__ __attribute__((aligned(16))) float sS[2][4][2][TSS]; // {kd, km, vd, vm} x block x token
+    __shared__ __attribute__((aligned(16))) _Float16 sV[3][TSS * RSV];
+    // block scales {d, m} x block x token of quantized K (per K buffer) and V (per V buffer)
+    __shared__ __attribute__((aligned(16))) float sSK[is_quant(KT) ? 2 : 1][2][2][is_quant(KT) ? TSS : 1];
+    __shared__ __attribute__((aligned(16))) float sSV[is_quant(VT) ? 3 : 1][2][2][is_quant(VT) ? TSS : 1];
 
     const FaUniform &U = args.u;
     FaProblem P;
@@ -332,20 +337,24 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
     constexpr float kbias = stage_bias<KT>();
 
     // unpack a staged tile's blocks (tokens t0..t0+TS) into LDS buffer `buf`
-    auto write_tile = [&](const RawBuf<W> &r, int buf, int t0) {
+    // (step: the step of the tile: K buffer step&1, V buffer step%3)
+    auto write_tile = [&](const RawBuf<W> &r, int step, int t0) {
         float d, m;
+        const int buf = step & 1, vbuf = step % 3;
         if (stage_k) {
             blk_stage<KT, false>(r, sK[buf] + st_tok * RSK + 32 * st_b);
             blk_scales<KT>(r, d, m);
-            sS[buf][0][st_b][st_tok] = d * smul;
-            if constexpr (has_min(KT)) sS[buf][1][st_b][st_tok] = m * smul;
+            if constexpr (is_quant(KT)) {
+                sSK[buf][0][st_b][st_tok] = d * smul;
+                if constexpr (has_min(KT)) sSK[buf][1][st_b][st_tok] = m * smul;
+            }
         } else if constexpr (VTR) {
             // dim-major rows of fp16; tokens from n_kv on are zeroed (the cache row continues
             // past them with whatever the cache holds, and they meet zero weights)
             const int nvalid = P.n_kv - t0 - VCH * vt_tc; // valid tokens of each run
 #pragma unroll
             for (int i = 0; i < VNCH; i++) {
-                _Float16 *dst = sV[buf] + (vt_d0 + VDSTEP * i) * RSV + VCH * vt_tc;
+                _Float16 *dst = sV[vbuf] + (vt_d0 + VDSTEP * i) * RSV + VCH * vt_tc;
                 if constexpr (VT == T_VT_F16) {
                     u4 w = {r.w[4 * i], r.w[4 * i + 1], r.w[4 * i + 2], r.w[4 * i + 3]};
                     if (t0 + TSS > P.n_kv) { // uniform: the cache's last tile
@@ -362,10 +371,12 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
                 }
             }
         } else {
-            blk_stage<VT, true>(r, sV[buf] + st_tok * RSV + 32 * st_b);
+            blk_stage<VT, true>(r, sV[vbuf] + st_tok * RSV + 32 * st_b);
             blk_scales<VT>(r, d, m);
-            sS[buf][2][st_b][st_tok] = d;
-            if constexpr (has_min(VT)) sS[buf][3][st_b][st_tok] = m;
+            if constexpr (is_quant(VT)) {
+                sSV[vbuf][0][st_b][st_tok] = d;
+                if constexpr (has_min(VT)) sSV[vbuf][1][st_b][st_tok] = m;
+            }
         }
     };
 
@@ -394,13 +405,16 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
         for (int i = 0; i < 4; i++) oacc[r][i] = f4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 
-    // compute one staged tile (LDS buffer `buf`, tokens t0..t0+TS) for both row sets; `full_c`
-    // (std::true_type) says every token of the tile is in range, so no bounds code is emitted
-    // (t0: this wave's 64 tokens, key half hk of the staged step)
-    auto compute_tile = [&](int buf, int t0, auto full_c) {
-        const _Float16 *cK = sK[buf] + hk * TS * RSK;
-        const _Float16 *cV = sV[buf] + hk * TS * RSV;
-        auto cS = [&](int x, int b) { return &sS[buf][x][b][hk * TS]; };
+    // P^T operands of the last tile, kept until its PV product (after the step's barrier)
+    h8 pb[NR][NKB][2];
+
+    // QK and softmax of one staged tile for both row sets (K buffer kb, V scales of V buffer vb,
+    // tokens t0..t0+TS), leaving its P^T operands in pb; `full_c` (std::true_type) says every
+    // token of the tile is in range, so no bounds code is emitted (t0: this wave's 64 tokens, key
+    // half hk of the staged step).  False when the mask removes the whole tile for this wave.
+    auto qk_soft = [&](int kb, int vb, int t0, auto full_c) -> bool {
+        const _Float16 *cK = sK[kb] + hk * TS * RSK;
+        auto cS = [&](int x, int b) { return x < 2 ? &sSK[kb][x][b][hk * TS] : &sSV[vb][x - 2][b][hk * TS]; };
         constexpr bool full = decltype(full_c)::value;
         // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
         // causal prefill) contributes nothing; the wave skips it
@@ -417,7 +431,7 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
                         live |= row_ok[r] && ((mwv[r][tt][0] & 0xffffu) != 0xfc00u || (mwv[r][tt][0] >> 16) != 0xfc00u ||
                                               (mwv[r][tt][1] & 0xffffu) != 0xfc00u || (mwv[r][tt][1] >> 16) != 0xfc00u);
                     }
-                if (__builtin_amdgcn_ballot_w64(live) == 0) return; // uniform
+                if (__builtin_amdgcn_ballot_w64(live) == 0) return false; // uniform
             }
         }
         f4 s[NR][NTILE];
@@ -474,7 +488,6 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
         // scales); the mask path turns them into base-2 logits here, the others in the exponent
         float sm2 = is_quant(KT) || MASK ? 1.0f : smul;
         const float mmul = is_quant(KT) ? 1.0f : smul;
-        h8 pb[NR][NKB][2];
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             // ---- mask, bounds, softmax with a lazily raised reference maximum ----
@@ -565,7 +578,13 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
             }
         }
 
-        // ---- O^T += V^T P^T: each V^T operand (two ds_read_b64_tr_b16) serves both row sets ----
+        return true;
+    };
+
+    // ---- O^T += V^T P^T for the tile whose P^T operands are in pb (V buffer vb): each V^T
+    //      operand (two ds_read_b64_tr_b16) serves every row set ----
+    auto pv = [&](int vb) {
+        const _Float16 *cV = sV[vb] + hk * TS * RSV;
 #pragma unroll
         for (int kb = 0; kb < NKB; kb++) {
             const int vrow = 32 * kb + 4 * g + (col >> 2);
@@ -598,30 +617,37 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
         }
     };
 
-    // ---- pipeline: tile s computes from LDS while tile s+1 is unpacked into the other buffer
-    //      from registers loaded two steps earlier ----
+    // ---- pipeline: step s runs the PV product of tile s-1 (V buffer (s-1)%3, its operands kept
+    //      in pb across the barrier), then QK and softmax of tile s (K buffer s&1), while tile
+    //      s+1 is unpacked into K buffer (s+1)&1 and V buffer (s+1)%3 from registers loaded two
+    //      steps earlier; no buffer is written in the step that reads it ----
     if (nsteps > 0) {
         write_tile(R0, 0, t_begin);
         if (nsteps > 2) load_tile(t_begin + 2 * TSS, R0);
     }
     __syncthreads();
     // full steps run in the loop; only the last step can be partial, and it runs after the loop
-    // from the buffer the loop staged it into
+    // from the buffers the loop staged it into
     const int nfull = max(0, t_end - t_begin) / TSS; // uniform
     const int t_half = hk * TS;                      // this wave's tokens within a step
+    bool pend = false; // pb holds a tile whose PV product has not run (uniform per wave)
+    auto step_full = [&](int s_) {
+        if (pend) pv((s_ + 2) % 3); // tile s_-1
+        pend = qk_soft(s_ & 1, s_ % 3, t_begin + s_ * TSS + t_half, std::true_type{});
+    };
     for (int s0 = 0; s0 < nfull; s0 += 2) {
-        // even step: compute buffer 0, stage step s0+1 (R1) into buffer 1
-        compute_tile(0, t_begin + s0 * TSS + t_half, std::true_type{});
+        // even step: stage step s0+1 from R1
+        step_full(s0);
         if (s0 + 1 < nsteps) {
-            write_tile(R1, 1, t_begin + (s0 + 1) * TSS);
+            write_tile(R1, s0 + 1, t_begin + (s0 + 1) * TSS);
             if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TSS, R1);
         }
         __syncthreads();
         if (s0 + 1 >= nfull) break;
-        // odd step: compute buffer 1, stage step s0+2 (R0) into buffer 0
-        compute_tile(1, t_begin + (s0 + 1) * TSS + t_half, std::true_type{});
+        // odd step: stage step s0+2 from R0
+        step_full(s0 + 1);
         if (s0 + 2 < nsteps) {
-            write_tile(R0, 0, t_begin + (s0 + 2) * TSS);
+            write_tile(R0, s0 + 2, t_begin + (s0 + 2) * TSS);
             if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TSS, R0);
         }
         __syncthreads();
@@ -630,13 +656,16 @@ __global__ __launch_bounds__(64 * ROWS_NW * KH) void fa_rows_kernel(FaArgs args)
         // the partial last step: with two key halves, a half's 64 tokens may be full, partial or
         // past the end (uniform per wave)
         const int t0w = t_begin + nfull * TSS + t_half;
+        if (pend) pv((nfull + 2) % 3);
         if constexpr (KH == 1) {
-            compute_tile(nfull & 1, t0w, std::false_type{});
+            pend = qk_soft(nfull & 1, nfull % 3, t0w, std::false_type{});
         } else {
-            if (t0w + TS <= t_end) compute_tile(nfull & 1, t0w, std::true_type{});
-            else if (t0w < t_end) compute_tile(nfull & 1, t0w, std::false_type{});
+            if (t0w + TS <= t_end) pend = qk_soft(nfull & 1, nfull % 3, t0w, std::true_type{});
+            else if (t0w < t_end) pend = qk_soft(nfull & 1, nfull % 3, t0w, std::false_type{});
+            else pend = false;
         }
     }
+    if (pend) pv((nsteps - 1) % 3);
 
     // unquantized V: this lane's share of the row sum (the row's lane group 0 holds it all)
     if constexpr (!is_quant(VT)) {
