@@ -185,20 +185,25 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 // launches with fewer row groups than CUs (prefill), where one wave per SIMD walks the whole key
 // range, this halves the chain each wave runs.
 template <int KT, int VT, bool MASK, bool BATCH, int KH>
-__global__ __launch_bounds__(64 * ROWS_NW * KH) __attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 ? 3 : 1)))
+__global__ __launch_bounds__(64 * ROWS_NW * KH)
+__attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 ? 3 : 1))) // 3 per SIMD: 168 VGPRs
 void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int TSS = TS * KH; // tokens per staged step
     constexpr int RSK = ROWS_RS, RSV = is_vt(VT) ? ROWS_RS_VT : ROWS_RS;
     static_assert(KH == 1 || (KH == 2 && !is_vt(VT)), "the transposed-V tile holds one 64-token step");
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
-    // K tiles double-buffered, V tiles triple-buffered: the PV product of tile s runs after the
-    // barrier that ends step s, beside the QK product of tile s+1, while step s+1 stages tile s+2
+    // SHIFT (f16 K and V): the PV product of tile s runs after the barrier that ends step s,
+    // beside the QK product of tile s+1, while step s+1 stages tile s+2, so the V tiles are
+    // triple-buffered.  The other type pairs run PV in the tile's own step (their P^T operands
+    // held across the barrier cost more registers than the overlap gains) with two V buffers.
+    constexpr bool SHIFT = KT == T_F16 && VT == T_F16;
+    constexpr int NVB = SHIFT ? 3 : 2;
     __shared__ __attribute__((aligned(16))) _Float16 sK[2][TSS * RSK];
-    __shared__ __attribute__((aligned(16))) _Float16 sV[3][TSS * RSV];
+    __shared__ __attribute__((aligned(16))) _Float16 sV[NVB][TSS * RSV];
     // block scales {d, m} x block x token of quantized K (per K buffer) and V (per V buffer)
     __shared__ __attribute__((aligned(16))) float sSK[is_quant(KT) ? 2 : 1][2][2][is_quant(KT) ? TSS : 1];
-    __shared__ __attribute__((aligned(16))) float sSV[is_quant(VT) ? 3 : 1][2][2][is_quant(VT) ? TSS : 1];
+    __shared__ __attribute__((aligned(16))) float sSV[is_quant(VT) ? NVB : 1][2][2][is_quant(VT) ? TSS : 1];
 
     const FaUniform &U = args.u;
     FaProblem P;
@@ -338,10 +343,10 @@ void fa_rows_kernel(FaArgs args) {
     constexpr float kbias = stage_bias<KT>();
 
     // unpack a staged tile's blocks (tokens t0..t0+TS) into LDS buffer `buf`
-    // (step: the step of the tile: K buffer step&1, V buffer step%3)
+    // (step: the step of the tile: K buffer step&1, V buffer step%NVB)
     auto write_tile = [&](const RawBuf<W> &r, int step, int t0) {
         float d, m;
-        const int buf = step & 1, vbuf = step % 3;
+        const int buf = step & 1, vbuf = step % NVB;
         if (stage_k) {
             blk_stage<KT, false>(r, sK[buf] + st_tok * RSK + 32 * st_b);
             blk_scales<KT>(r, d, m);
@@ -631,10 +636,14 @@ void fa_rows_kernel(FaArgs args) {
     // from the buffers the loop staged it into
     const int nfull = max(0, t_end - t_begin) / TSS; // uniform
     const int t_half = hk * TS;                      // this wave's tokens within a step
-    bool pend = false; // pb holds a tile whose PV product has not run (uniform per wave)
+    bool pend = false; // SHIFT: pb holds a tile whose PV product has not run (uniform per wave)
     auto step_full = [&](int s_) {
-        if (pend) pv((s_ + 2) % 3); // tile s_-1
-        pend = qk_soft(s_ & 1, s_ % 3, t_begin + s_ * TSS + t_half, std::true_type{});
+        if constexpr (SHIFT) {
+            if (pend) pv((s_ + NVB - 1) % NVB); // tile s_-1
+            pend = qk_soft(s_ & 1, s_ % NVB, t_begin + s_ * TSS + t_half, std::true_type{});
+        } else {
+            if (qk_soft(s_ & 1, s_ % NVB, t_begin + s_ * TSS + t_half, std::true_type{})) pv(s_ % NVB);
+        }
     };
     for (int s0 = 0; s0 < nfull; s0 += 2) {
         // even step: stage step s0+1 from R1
@@ -657,16 +666,21 @@ void fa_rows_kernel(FaArgs args) {
         // the partial last step: with two key halves, a half's 64 tokens may be full, partial or
         // past the end (uniform per wave)
         const int t0w = t_begin + nfull * TSS + t_half;
-        if (pend) pv((nfull + 2) % 3);
+        if (pend) pv((nfull + NVB - 1) % NVB);
+        const int kb = nfull & 1, vb = nfull % NVB;
         if constexpr (KH == 1) {
-            pend = qk_soft(nfull & 1, nfull % 3, t0w, std::false_type{});
+            pend = qk_soft(kb, vb, t0w, std::false_type{});
         } else {
-            if (t0w + TS <= t_end) pend = qk_soft(nfull & 1, nfull % 3, t0w, std::true_type{});
-            else if (t0w < t_end) pend = qk_soft(nfull & 1, nfull % 3, t0w, std::false_type{});
+            if (t0w + TS <= t_end) pend = qk_soft(kb, vb, t0w, std::true_type{});
+            else if (t0w < t_end) pend = qk_soft(kb, vb, t0w, std::false_type{});
             else pend = false;
         }
+        if constexpr (!SHIFT) {
+            if (pend) pv(vb);
+            pend = false;
+        }
     }
-    if (pend) pv((nsteps - 1) % 3);
+    if (pend) pv((nsteps - 1) % NVB);
 
     // unquantized V: this lane's share of the row sum (the row's lane group 0 holds it all)
     if constexpr (!is_quant(VT)) {
