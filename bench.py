@@ -142,6 +142,32 @@ def bench_dit(lib, cvattn, torch, dev, iters=50):
     return {"ms_per_layer_call": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flop_per_call": flops, "calls": n}
 
 
+def bench_dit_f32_views(lib, cvattn, torch, dev, iters=50):
+    """The same DiT call in the form the flow graph passes it (src/cosyvoice-graph.cpp:370-376):
+    fp32 q/k/v views of the rope and linear outputs, one cvattn_flash_attn_ext call with its
+    workspace (which holds the fp16 copies of K and V made inside the call)."""
+    T, B, HD = 1500, 2, 16
+    q = torch.randn((B, T, HD * D), device=dev)
+    k = torch.randn((B, T, HD * D), device=dev)
+    v = torch.randn((B, T, HD * D), device=dev)
+    out = torch.empty((B, T, HD, D), device=dev, dtype=torch.float32)
+    qv = cvattn.dit_view(q.data_ptr(), T, B, ttype=cvattn.F32)
+    kv = cvattn.dit_view(k.data_ptr(), T, B, ttype=cvattn.F32)
+    vv = cvattn.dit_view(v.data_ptr(), T, B, ttype=cvattn.F32)
+    dst = cvattn.out_view(out.data_ptr(), D, HD, T, B)
+    nws = lib.flash_attn_ext_workspace(qv, kv, vv, None)
+    ws = torch.empty(max(1, nws), dtype=torch.uint8, device=dev)
+
+    def launch(s):
+        for _ in range(10):
+            assert lib.flash_attn_ext(qv, kv, vv, None, dst, 0.125, ws.data_ptr(), nws, s) == cvattn.OK
+
+    ms, n = time_graph(torch, launch, 10, iters, 10)
+    flops = 4.0 * D * B * HD * T * T
+    return {"workload": "flow-DiT attention layer call, T=1500, batch 2, 16 heads, fp32 q/k/v views, single call",
+            "us_per_layer_call": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12, "workspace_bytes": nws, "calls": n}
+
+
 def bench_prefill(lib, cvattn, torch, dev, iters=48):
     """LLM prefill layer call: 1024 query tokens over 1024 f16 cached tokens, causal mask, 14/2 heads
     (Q, K, V ~ 0.5 N(0,1)); 24 layers of the same shape are cycled."""
@@ -429,6 +455,10 @@ def main():
     if dit:
         log(f"dit T=1500: {dit['ms_per_layer_call'] * 1e3:.1f} us/call, {dit['tflops']:.1f} TFLOP/s")
     extra = {}
+    if not args.no_extra and not args.no_dit:
+        extra["dit_attn_f32_views"] = bench_dit_f32_views(lib, cvattn, torch, dev)
+        log(f"dit T=1500 fp32 views: {extra['dit_attn_f32_views']['us_per_layer_call']:.1f} us/call, "
+            f"{extra['dit_attn_f32_views']['tflops']:.1f} TFLOP/s")
     if not args.no_extra:
         extra["prefill_attn"] = bench_prefill(lib, cvattn, torch, dev)
         log(f"prefill 1024 causal: {extra['prefill_attn']['us_per_layer_call']:.1f} us/layer, "

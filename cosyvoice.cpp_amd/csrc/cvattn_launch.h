@@ -28,6 +28,20 @@ hipError_t fa_launch_vt(int ktype, int vtype, bool mask, const FaArgs &a, hipStr
 
 hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st);
 
+// fp32 -> fp16 copy (round to nearest even, the conversion the attention kernels apply when
+// they stage fp32 K/V) of a strided 4-d view [ne0, ne1, ne2, ne3] into dense rows of dst_row
+// halfs (a multiple of 8; the pad of a row is written as zeros).
+struct CvtF16Args {
+    const uint8_t *src;
+    _Float16 *dst;
+    int64_t ne0, ne1, ne2;
+    int64_t nb1, nb2, nb3;
+    int64_t dst_row;
+    int64_t chunks;   // dst_row / 8: one thread per 8 halfs of a row
+    int64_t total;    // rows * chunks
+};
+hipError_t cvt_f16_launch(const CvtF16Args &a, hipStream_t st);
+
 struct SetRowsArgs {
     uint8_t *dst;
     const uint8_t *src;

@@ -8,9 +8,12 @@
 // of 16 rows (the 16 columns of its MFMA tiles); each K or V operand read from LDS feeds one MFMA
 // per set.  A workgroup is 4 waves (64 rows with one set) sharing 64-token K/V tiles that are
 // staged once per step into LDS from registers loaded two steps ahead, so a step has one
-// barrier.  Step s runs the PV product of tile s-1 (its P^T operands kept in registers across
-// the barrier), then QK and softmax of tile s, while tile s+1 is unpacked: K tiles are
-// double-buffered and V tiles triple-buffered, so no buffer is written in a step that reads it.  With two key halves (KH = 2, for launches with fewer row groups than CUs) a
+// barrier.  With f16 K and V, step s runs the PV product of tile s-1 (its P^T operands kept in
+// registers across the barrier), then QK and softmax of tile s, while tile s+1 is unpacked: K
+// tiles are double-buffered and V tiles triple-buffered, so no buffer is written in a step that
+// reads it.  The other type pairs run QK, softmax and PV of tile s in step s with two V buffers
+// (their wider staging leaves no registers for P^T across the barrier).  With two key halves
+// (KH = 2, for launches with fewer row groups than CUs) a
 // workgroup is 8 waves: a step stages 128 tokens, waves w and w+4 compute the two 64-token
 // halves for the same rows, and the halves are merged through LDS at the end.
 //

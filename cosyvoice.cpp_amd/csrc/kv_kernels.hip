@@ -6,7 +6,9 @@
 //     with the K rotary embedding of the same layer fused in front (src/cosyvoice-llm.cpp:57,
 //     src/cosyvoice-graph.cpp:352);
 //   * rope: ggml_rope_ext for the query side (src/cosyvoice-llm.cpp:56,
-//     src/cosyvoice-graph.cpp:351).
+//     src/cosyvoice-graph.cpp:351);
+//   * cvt_f16: the one-time fp16 copy of fp32 K/V views that many row groups read (the DiT
+//     call without cache, src/cosyvoice-graph.cpp:370-376).
 #include "cvattn_device.h"
 #include "cvattn_launch.h"
 
@@ -55,6 +57,34 @@ __global__ __launch_bounds__(256) void copy_f32_kernel(const float *src, float *
 __global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16 *src, float *dst, int64_t n) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) dst[i] = (float)src[i];
+}
+
+// One thread per 8 halfs of a destination row.  VEC: the source rows are 16-byte aligned and
+// ne0 is a multiple of 8, so a chunk is two 16-byte loads.
+template <bool VEC>
+__global__ __launch_bounds__(256) void cvt_f16_kernel(CvtF16Args a) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= a.total) return;
+    const int64_t r = t / a.chunks, i0 = 8 * (t - r * a.chunks);
+    const int64_t i1 = r % a.ne1, r2 = r / a.ne1;
+    const int64_t i2 = r2 % a.ne2, i3 = r2 / a.ne2;
+    const float *row = (const float *)(a.src + i1 * a.nb1 + i2 * a.nb2 + i3 * a.nb3);
+    float x[8];
+    if constexpr (VEC) {
+        const f4 lo = *(const f4 *)(row + i0), hi = *(const f4 *)(row + i0 + 4);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            x[j] = lo[j];
+            x[4 + j] = hi[j];
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; j++) x[j] = i0 + j < a.ne0 ? row[i0 + j] : 0.0f;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) o[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)x[2 * j], (_Float16)x[2 * j + 1]});
+    *(u4 *)(a.dst + r * a.dst_row + i0) = u4{o[0], o[1], o[2], o[3]};
 }
 
 // ------------------------------------------------------------------------------------------
@@ -390,6 +420,16 @@ static hipError_t set_rows_launch_t(int type, const SetRowsArgs &a, hipStream_t 
 hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st) {
     if (a.total <= 0) return hipSuccess;
     return a.rope_dims > 0 ? set_rows_launch_t<true>(type, a, st) : set_rows_launch_t<false>(type, a, st);
+}
+
+hipError_t cvt_f16_launch(const CvtF16Args &a, hipStream_t st) {
+    if (a.total <= 0) return hipSuccess;
+    const int64_t blocks = (a.total + 255) / 256;
+    if (blocks > INT32_MAX || a.dst_row % 8 || a.chunks * 8 != a.dst_row || a.ne0 > a.dst_row) return hipErrorInvalidValue;
+    const bool vec = a.ne0 % 8 == 0 && (((uintptr_t)a.src | (uintptr_t)a.nb1 | (uintptr_t)a.nb2 | (uintptr_t)a.nb3) & 15) == 0;
+    if (vec) hipLaunchKernelGGL(cvt_f16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(cvt_f16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+    return hipGetLastError();
 }
 
 hipError_t rope_launch(const RopeArgs &a, hipStream_t st) {

@@ -87,8 +87,9 @@ typedef struct cvattn_tensor {
 CVATTN_API int cvattn_supports_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
                                               const cvattn_tensor *v, const cvattn_tensor *mask);
 
-/* Bytes of device workspace cvattn_flash_attn_ext needs for these shapes (the partial results
- * of a KV sequence split over several workgroups).  0 is a valid answer. */
+/* Bytes of device workspace cvattn_flash_attn_ext needs for these shapes: the partial results
+ * of a KV sequence split over several workgroups, and fp16 copies of fp32 K/V that many query
+ * row groups read (the DiT call without cache).  0 is a valid answer. */
 CVATTN_API size_t cvattn_flash_attn_ext_workspace(const cvattn_tensor *q, const cvattn_tensor *k,
                                                   const cvattn_tensor *v, const cvattn_tensor *mask);
 

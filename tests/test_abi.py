@@ -92,6 +92,30 @@ def test_workspace_and_errors(eng):
     assert eng.flash_attn_ext_workspace(q, k, v, None) == 0
 
 
+def test_workspace_holds_fp16_copies_of_fp32_kv(eng):
+    """fp32 K/V read by many row groups (the DiT call without cache) are copied to fp16 in the
+    workspace: 64 halfs per K/V row, token rows of the transposed V padded to 8 halfs."""
+    T, H, B = 1500, 16, 2
+
+    def dit(t, n=T):
+        es = 4 if t == F32 else 2
+        return cvattn.tensor(FAKE, t, [64, n, H, B], [es, es * 64 * H, es * 64, es * 64 * H * n])
+
+    rows = T * H * B
+    assert eng.flash_attn_ext_workspace(dit(F16), dit(F16), dit(F16), None) == 0
+    assert eng.flash_attn_ext_workspace(dit(F32), dit(F32), dit(F16), None) == rows * 64 * 2
+    both = eng.flash_attn_ext_workspace(dit(F32), dit(F32), dit(F32), None)
+    assert both == 2 * rows * 64 * 2  # K copy (256-byte aligned size) then V copy
+    assert eng.flash_attn_ext_workspace(dit(F32), dit(F16), dit(F32), None) == rows * 64 * 2
+    # a short query run (a single row group) stages fp32 directly
+    assert eng.flash_attn_ext_workspace(dit(F32, 50), dit(F32, 50), dit(F32, 50), None) == 0
+    # transposed V of the non-flash form: [T, 64, H, B] with T = 301 -> rows of 304 halfs
+    n = 301
+    vt = cvattn.tensor(FAKE, F32, [n, 64, H, B], [4, 4 * n, 4 * n * 64, 4 * n * 64 * H])
+    k = dit(F32, n)
+    assert eng.attn_nonfa_workspace(dit(F32, n), k, vt, None) == n * H * B * 64 * 2 + 64 * H * B * 304 * 2
+
+
 def test_batch_validation(eng):
     probs = []
     for n_kv in (256, 1000, 8192):

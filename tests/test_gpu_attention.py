@@ -232,6 +232,23 @@ def test_dit_f16_inputs(eng, orc, rng, cuda):
     run_case(eng, orc, c, what="dit f16")
 
 
+@pytest.mark.parametrize("kt,vt", [(F32, F16), (F16, F32)])
+def test_dit_one_fp32_side(eng, orc, rng, kt, vt, cuda):
+    """Only one of K/V fp32: that side alone is copied to fp16 before the kernel runs."""
+    T, B, H = 400, 2, 16
+    c = Case()
+    for name, t, n in (("q", F32, T), ("k", kt, T), ("v", vt, T)):
+        x = rng.standard_normal((B, n, H * D)).astype(np.float32)
+        es = 4 if t == F32 else 2
+        arr = x if t == F32 else orc.f32_to_f16(x)
+        c.add(name, arr, t, [D, n, H, B], [es, es * H * D, es * D, es * H * D * n])
+    c.mask_h = c.mask_d = None
+    c.out_shape = (B, T, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, T, B)
+    run_case(eng, orc, c, what=f"dit k{kt} v{vt}")
+
+
 def test_dit_chunk_mask(eng, orc, rng, cuda):
     T = 250
     mask = orc.chunk_mask(T, [50, 100, 150, 200])

@@ -78,10 +78,12 @@ def test_llm_prefill_nonfa_causal(eng, orc, rng, cuda, nq, nkv):
     check_close(host(out), want, what=f"nonfa prefill {nq}x{nkv}")
 
 
-def test_dit_nonfa_no_cache(eng, orc, rng, cuda):
+@pytest.mark.parametrize("T", [300, 301])
+def test_dit_nonfa_no_cache(eng, orc, rng, cuda, T):
     """DiT without cache: q/k the f32 [64, T, 16, 2] views, V transposed by the ggml_cont of
-    permute(1, 0, 2, 3) into [T, 64, 16, 2] (src/cosyvoice-graph.cpp:380-381)."""
-    T, B, H = 300, 2, 16
+    permute(1, 0, 2, 3) into [T, 64, 16, 2] (src/cosyvoice-graph.cpp:380-381).  Both are copied
+    to fp16 first; an odd T pads the copied V rows."""
+    B, H = 2, 16
     h = Held()
     x = rng.standard_normal((3, B, T, H * D)).astype(np.float32)
     ne = [D, T, H, B]
