@@ -266,7 +266,7 @@ struct SinglePlan {
 
 // fp32 K/V read by at least this many row groups are copied once to fp16 in the workspace
 // before the row-tiled kernel runs: the kernel stages fp32 tiles by converting them to fp16
-// anyway (the copy rounds the same way, so results are unchanged), and staging fp32 holds
+// anyway (the copy rounds the same way, so the staged tiles are the same), and staging fp32 holds
 // twice the registers, which keeps fewer workgroups resident (DiT T=1500, 16 heads, batch 2:
 // 84-90 us from fp32 views, 43 us from fp16 K/V).  The copy costs one pass over K/V, paid back
 // when several row groups re-read every tile.
