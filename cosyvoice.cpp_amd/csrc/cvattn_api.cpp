@@ -292,8 +292,10 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
         plan_splits(sh, sh.n_kv, split_work(sh), &pl->n_splits, &pl->split_len, false);
     size_t bytes = pl->n_splits > 1 ? (size_t)slots_per_split(sh) * pl->n_splits * PART_STRIDE * sizeof(float) : 0;
     const bool many = !sh.ks.wsplit && sh.n_rowgroups >= kCvtMinRowGroups;
-    pl->cvt_k = many && k->type == T_F32;
-    pl->cvt_v = many && v->type == T_F32;
+    // the transposed V's rows are its tokens: padded to 8 halfs, so they stay 16-byte aligned
+    const int64_t v_row = vt ? (v->ne[0] + 7) / 8 * 8 : HEAD;
+    pl->cvt_k = many && k->type == T_F32 && view_rows(k) * (HEAD / 8) <= kCvtMaxChunks;
+    pl->cvt_v = many && v->type == T_F32 && view_rows(v) * (v_row / 8) <= kCvtMaxChunks;
     pl->k_off = pl->v_off = 0;
     pl->v_row = 0;
     if (pl->cvt_k) {
@@ -301,8 +303,7 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
         bytes += (size_t)view_rows(k) * HEAD * sizeof(_Float16);
     }
     if (pl->cvt_v) {
-        // the transposed V's rows are its tokens: padded to 8 halfs, so they stay 16-byte aligned
-        pl->v_row = vt ? (v->ne[0] + 7) / 8 * 8 : HEAD;
+        pl->v_row = v_row;
         pl->v_off = bytes = align_up(bytes, kAlign);
         bytes += (size_t)view_rows(v) * (size_t)pl->v_row * sizeof(_Float16);
     }
@@ -310,10 +311,9 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
     return CVATTN_OK;
 }
 
-// Copy an fp32 view into the workspace as dense fp16 rows of `row` halfs and describe the copy
-// as a view of the same shape.
-int copy_to_f16(const cvattn_tensor *t, uint8_t *dst, int64_t row, cvattn_tensor *out, hipStream_t st) {
-    CvtF16Args c;
+// Describe the copy of an fp32 view into the workspace as dense fp16 rows of `row` halfs (`c`,
+// for cvt_f16_launch) and the copy as a view of the same shape (`out`).
+void copy_to_f16(const cvattn_tensor *t, uint8_t *dst, int64_t row, CvtF16Args &c, cvattn_tensor *out) {
     c.src = (const uint8_t *)t->data;
     c.dst = (_Float16 *)dst;
     c.ne0 = t->ne[0];
@@ -332,7 +332,6 @@ int copy_to_f16(const cvattn_tensor *t, uint8_t *dst, int64_t row, cvattn_tensor
     out->nb[1] = (size_t)row * sizeof(_Float16);
     out->nb[2] = out->nb[1] * (size_t)t->ne[1];
     out->nb[3] = out->nb[2] * (size_t)t->ne[2];
-    return cvt_f16_launch(c, st) == hipSuccess ? CVATTN_OK : CVATTN_ERR_HIP;
 }
 
 // Host-side launch plan for batches (stored in cvattn_fa_plan::opaque).
@@ -391,16 +390,17 @@ static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvat
     if (rc) return rc;
     if (ws_bytes < pl.ws_bytes || (pl.ws_bytes && !ws)) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
     cvattn_tensor k16, v16;
+    CvtF16Args cvt[2];
+    int n_cvt = 0;
     if (pl.cvt_k) {
-        rc = copy_to_f16(k, (uint8_t *)ws + pl.k_off, HEAD, &k16, (hipStream_t)stream);
-        if (rc) return rc;
+        copy_to_f16(k, (uint8_t *)ws + pl.k_off, HEAD, cvt[n_cvt++], &k16);
         k = &k16;
     }
     if (pl.cvt_v) {
-        rc = copy_to_f16(v, (uint8_t *)ws + pl.v_off, pl.v_row, &v16, (hipStream_t)stream);
-        if (rc) return rc;
+        copy_to_f16(v, (uint8_t *)ws + pl.v_off, pl.v_row, cvt[n_cvt++], &v16);
         v = &v16;
     }
+    if (n_cvt && cvt_f16_launch(cvt, n_cvt, (hipStream_t)stream) != hipSuccess) return CVATTN_ERR_HIP;
     FaArgs a;
     std::memset(&a, 0, sizeof(a));
     fill_uniform(a.u, pl.sh, q->type, scale);

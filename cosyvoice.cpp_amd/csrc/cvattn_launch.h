@@ -30,7 +30,8 @@ hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipS
 
 // fp32 -> fp16 copy (round to nearest even, the conversion the attention kernels apply when
 // they stage fp32 K/V) of a strided 4-d view [ne0, ne1, ne2, ne3] into dense rows of dst_row
-// halfs (a multiple of 8; the pad of a row is written as zeros).
+// halfs (a multiple of 8; the pad of a row is written as zeros).  total < 2^31: the kernel
+// indexes with 32-bit fast divisions.
 struct CvtF16Args {
     const uint8_t *src;
     _Float16 *dst;
@@ -39,8 +40,11 @@ struct CvtF16Args {
     int64_t dst_row;
     int64_t chunks;   // dst_row / 8: one thread per 8 halfs of a row
     int64_t total;    // rows * chunks
+    FastDiv div_chunks, div_ne1, div_ne2;   // filled by cvt_f16_launch
 };
-hipError_t cvt_f16_launch(const CvtF16Args &a, hipStream_t st);
+constexpr int64_t kCvtMaxChunks = INT32_MAX;
+// Copies n (1 or 2) views in one launch: the K and V copies of one attention call.
+hipError_t cvt_f16_launch(CvtF16Args *a, int n, hipStream_t st);
 
 struct SetRowsArgs {
     uint8_t *dst;

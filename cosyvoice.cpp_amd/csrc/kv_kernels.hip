@@ -59,19 +59,28 @@ __global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16 *src, fl
     if (i < n) dst[i] = (float)src[i];
 }
 
-// One thread per 8 halfs of a destination row.  VEC: the source rows are 16-byte aligned and
-// ne0 is a multiple of 8, so a chunk is two 16-byte loads.
+// One thread per 8 halfs of a destination row; blocks [0, blocks0) copy view 0, the rest view 1
+// (the K and V copies of one call share a launch).  Indices are 32-bit (total < 2^31).  VEC: the
+// source rows are 16-byte aligned and ne0 is a multiple of 8, so a chunk is two 16-byte loads.
+// The source is read once (non-temporal loads); the copy stays cached for the attention kernel.
+struct CvtF16Pair {
+    CvtF16Args v[2];
+    uint32_t blocks0;
+};
 template <bool VEC>
-__global__ __launch_bounds__(256) void cvt_f16_kernel(CvtF16Args a) {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= a.total) return;
-    const int64_t r = t / a.chunks, i0 = 8 * (t - r * a.chunks);
-    const int64_t i1 = r % a.ne1, r2 = r / a.ne1;
-    const int64_t i2 = r2 % a.ne2, i3 = r2 / a.ne2;
-    const float *row = (const float *)(a.src + i1 * a.nb1 + i2 * a.nb2 + i3 * a.nb3);
+__global__ __launch_bounds__(256) void cvt_f16_kernel(CvtF16Pair p) {
+    const bool second = blockIdx.x >= p.blocks0;
+    const CvtF16Args &a = second ? p.v[1] : p.v[0];
+    const uint32_t t = (blockIdx.x - (second ? p.blocks0 : 0u)) * 256u + threadIdx.x;
+    if (t >= (uint32_t)a.total) return;
+    const uint32_t r = fdiv(t, a.div_chunks), i0 = 8u * (t - r * (uint32_t)a.chunks);
+    const uint32_t r2 = fdiv(r, a.div_ne1), i1 = r - r2 * (uint32_t)a.ne1;
+    const uint32_t i3 = fdiv(r2, a.div_ne2), i2 = r2 - i3 * (uint32_t)a.ne2;
+    const float *row = (const float *)(a.src + (int64_t)i1 * a.nb1 + (int64_t)i2 * a.nb2 + (int64_t)i3 * a.nb3);
     float x[8];
     if constexpr (VEC) {
-        const f4 lo = *(const f4 *)(row + i0), hi = *(const f4 *)(row + i0 + 4);
+        const f4 lo = __builtin_nontemporal_load((const f4 *)(row + i0));
+        const f4 hi = __builtin_nontemporal_load((const f4 *)(row + i0 + 4));
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             x[j] = lo[j];
@@ -79,12 +88,12 @@ __global__ __launch_bounds__(256) void cvt_f16_kernel(CvtF16Args a) {
         }
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; j++) x[j] = i0 + j < a.ne0 ? row[i0 + j] : 0.0f;
+        for (int j = 0; j < 8; j++) x[j] = i0 + j < (uint32_t)a.ne0 ? row[i0 + j] : 0.0f;
     }
     uint32_t o[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) o[j] = __builtin_bit_cast(uint32_t, h2{(_Float16)x[2 * j], (_Float16)x[2 * j + 1]});
-    *(u4 *)(a.dst + r * a.dst_row + i0) = u4{o[0], o[1], o[2], o[3]};
+    *(u4 *)(a.dst + (int64_t)r * a.dst_row + i0) = u4{o[0], o[1], o[2], o[3]};
 }
 
 // ------------------------------------------------------------------------------------------
@@ -422,13 +431,29 @@ hipError_t set_rows_launch(int type, const SetRowsArgs &a, hipStream_t st) {
     return a.rope_dims > 0 ? set_rows_launch_t<true>(type, a, st) : set_rows_launch_t<false>(type, a, st);
 }
 
-hipError_t cvt_f16_launch(const CvtF16Args &a, hipStream_t st) {
-    if (a.total <= 0) return hipSuccess;
-    const int64_t blocks = (a.total + 255) / 256;
-    if (blocks > INT32_MAX || a.dst_row % 8 || a.chunks * 8 != a.dst_row || a.ne0 > a.dst_row) return hipErrorInvalidValue;
-    const bool vec = a.ne0 % 8 == 0 && (((uintptr_t)a.src | (uintptr_t)a.nb1 | (uintptr_t)a.nb2 | (uintptr_t)a.nb3) & 15) == 0;
-    if (vec) hipLaunchKernelGGL(cvt_f16_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(cvt_f16_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+hipError_t cvt_f16_launch(CvtF16Args *a, int n, hipStream_t st) {
+    if (n < 1 || n > 2) return hipErrorInvalidValue;
+    CvtF16Pair p;
+    bool vec = true;
+    int64_t blocks[2] = {0, 0};
+    for (int i = 0; i < n; i++) {
+        CvtF16Args &c = a[i];
+        if (c.total < 0 || c.total > kCvtMaxChunks || c.dst_row % 8 || c.chunks * 8 != c.dst_row || c.ne0 > c.dst_row ||
+            c.ne1 <= 0 || c.ne2 <= 0)
+            return hipErrorInvalidValue;
+        c.div_chunks = make_fastdiv((uint32_t)c.chunks);
+        c.div_ne1 = make_fastdiv((uint32_t)c.ne1);
+        c.div_ne2 = make_fastdiv((uint32_t)c.ne2);
+        vec = vec && c.ne0 % 8 == 0 && (((uintptr_t)c.src | (uintptr_t)c.nb1 | (uintptr_t)c.nb2 | (uintptr_t)c.nb3) & 15) == 0;
+        blocks[i] = (c.total + 255) / 256;
+        p.v[i] = c;
+    }
+    if (n == 1) p.v[1] = p.v[0];
+    p.blocks0 = (uint32_t)blocks[0];
+    const int64_t grid = blocks[0] + blocks[1];
+    if (grid == 0) return hipSuccess;
+    if (vec) hipLaunchKernelGGL(cvt_f16_kernel<true>, dim3((unsigned)grid), dim3(256), 0, st, p);
+    else hipLaunchKernelGGL(cvt_f16_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, p);
     return hipGetLastError();
 }
 
