@@ -332,6 +332,86 @@ def test_batch_prefill_with_masks(eng, orc, rng, cuda):
         check_close(host(c.dst), want, what="batch prefill")
 
 
+def one_allocation(cases, names=("q", "k", "v", "mask")):
+    """Move the cases' tensors into one device allocation per tensor kind, problem i at a fixed
+    byte stride past problem i-1 (the layers of one cache buffer), and return their problems."""
+    keep = []
+    for name in names:
+        if getattr(cases[0], name + "_d", None) is None:
+            continue
+        big = torch.stack([getattr(c, name + "_dev") for c in cases])
+        keep.append(big)
+        for i, c in enumerate(cases):
+            t = getattr(c, name + "_d")
+            setattr(c, name + "_d", cvattn.tensor(big[i].data_ptr(), t.type, list(t.ne), list(t.nb)))
+    out = empty_f32(len(cases), *cases[0].out_shape)
+    keep.append(out)
+    for i, c in enumerate(cases):
+        c.dst = out[i]
+        B, nq, H, _ = c.out_shape
+        c.dst_d = cvattn.out_view(out[i].data_ptr(), D, H, nq, B)
+    probs = []
+    for c in cases:
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.dst = c.q_d, c.k_d, c.v_d, c.dst_d
+        if c.mask_d is not None:
+            p.mask = c.mask_d
+        probs.append(p)
+    return probs, keep
+
+
+def launch_batch(eng, probs):
+    ws = workspace(eng.fa_batch_workspace(probs))
+    rc, plan = eng.fa_batch_prepare(probs, 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    for _ in range(2):  # the merging workgroups leave the arrival counters at zero
+        assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    return ws
+
+
+@pytest.mark.parametrize("order", ["forward", "reversed", "broken"])
+def test_batch_layers_of_one_allocation(eng, orc, rng, order, cuda):
+    """Decode problems whose tensors sit at fixed strides in one allocation (the layers of one
+    cache buffer), in order, reversed, and with two swapped, give the oracle's results; two
+    launches of one plan (the merging workgroups reset the arrival counters) agree."""
+    cases = [llm_case(orc, rng, nq=1, nkv=1500, kt=Q8_0, vt=Q4_0, max_seq=1536) for _ in range(6)]
+    probs, keep = one_allocation(cases)
+    idx = list(range(6))
+    if order == "reversed":
+        idx = idx[::-1]
+    elif order == "broken":
+        idx[2], idx[3] = idx[3], idx[2]
+    launch_batch(eng, [probs[i] for i in idx])
+    for i, c in enumerate(cases):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"{order} layer {i}")
+
+
+def test_batch_masked_prefill_of_one_allocation(eng, orc, rng, cuda):
+    """Causal prefill problems (row-tiled kernel) with their masks, each kind of tensor in one
+    allocation."""
+    mask = orc.causal_mask(40, 300)
+    cases = [llm_case(orc, rng, nq=40, nkv=300, kt=F16, vt=Q8_0, mask=mask, max_seq=320) for _ in range(4)]
+    probs, keep = one_allocation(cases)
+    launch_batch(eng, probs)
+    for i, c in enumerate(cases):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"masked layer {i}")
+
+
+def test_decode_24_layer_step_one_allocation(eng, orc, cuda):
+    """The benchmark's decode step with its layers in one K and one V allocation (as the cache
+    buffer holds them): 24 layers x 4096 tokens, K q8_0 / V q4_0, one prepared batch."""
+    rng = np.random.default_rng(2027)
+    cases = [llm_case(orc, rng, nq=1, nkv=4096, kt=Q8_0, vt=Q4_0, max_seq=4096) for _ in range(24)]
+    probs, keep = one_allocation(cases)
+    launch_batch(eng, probs)
+    for i, c in enumerate(cases):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"24-layer step, layer {i}")
+
+
 def test_short_prefill_over_long_cache_splits(eng, orc, rng, cuda):
     """12 new tokens over a 3000-token q8_0/q4_0 cache: 84 rows per kv head run in the row-tiled
     kernel, and so few row groups over so many keys are split over tokens -- merged by a second
