@@ -61,8 +61,8 @@ __global__ __launch_bounds__(256) void f16_to_f32_kernel(const _Float16 *src, fl
 
 // One thread per 8 halfs of a destination row; blocks [0, blocks0) copy view 0, the rest view 1
 // (the K and V copies of one call share a launch).  Indices are 32-bit (total < 2^31).  VEC: the
-// source rows are 16-byte aligned and ne0 is a multiple of 8, so a chunk is two 16-byte loads.
-// The source is read once (non-temporal loads); the copy stays cached for the attention kernel.
+// source rows are 16-byte aligned and ne0 is a multiple of 8, so a chunk is two 16-byte loads
+// (plain loads: non-temporal ones made the T=1500 DiT call ~3 us slower).
 struct CvtF16Pair {
     CvtF16Args v[2];
     uint32_t blocks0;
@@ -79,8 +79,8 @@ __global__ __launch_bounds__(256) void cvt_f16_kernel(CvtF16Pair p) {
     const float *row = (const float *)(a.src + (int64_t)i1 * a.nb1 + (int64_t)i2 * a.nb2 + (int64_t)i3 * a.nb3);
     float x[8];
     if constexpr (VEC) {
-        const f4 lo = __builtin_nontemporal_load((const f4 *)(row + i0));
-        const f4 hi = __builtin_nontemporal_load((const f4 *)(row + i0 + 4));
+        const f4 lo = *(const f4 *)(row + i0);
+        const f4 hi = *(const f4 *)(row + i0 + 4);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             x[j] = lo[j];
