@@ -118,7 +118,7 @@ def time_graph(torch, launch_fn, n_per_graph, steps, warmup):
     return start.elapsed_time(end) / (reps * n_per_graph), reps * n_per_graph
 
 
-def bench_dit(lib, cvattn, torch, dev, iters=50):
+def bench_dit(lib, cvattn, torch, dev, iters=300):
     """Flow-DiT attention layer call: T=1500, B=2, 16 heads, fp16 q/k/v views, no mask."""
     T, B, HD = 1500, 2, 16
     q = torch.randn((B, T, HD * D), device=dev, dtype=torch.float16)
@@ -137,12 +137,12 @@ def bench_dit(lib, cvattn, torch, dev, iters=50):
         for _ in range(10):
             assert lib.fa_batch_launch(plan, s) == cvattn.OK
 
-    ms, n = time_graph(torch, launch, 10, iters, 10)
+    ms, n = time_graph(torch, launch, 10, iters, 100)
     flops = 4.0 * D * B * HD * T * T
     return {"ms_per_layer_call": ms, "tflops": flops / (ms * 1e-3) / 1e12, "flop_per_call": flops, "calls": n}
 
 
-def bench_dit_f32_views(lib, cvattn, torch, dev, iters=50):
+def bench_dit_f32_views(lib, cvattn, torch, dev, iters=300):
     """The same DiT call in the form the flow graph passes it (src/cosyvoice-graph.cpp:370-376):
     fp32 q/k/v views of the rope and linear outputs, one cvattn_flash_attn_ext call with its
     workspace (which holds the fp16 copies of K and V made inside the call)."""
@@ -162,13 +162,13 @@ def bench_dit_f32_views(lib, cvattn, torch, dev, iters=50):
         for _ in range(10):
             assert lib.flash_attn_ext(qv, kv, vv, None, dst, 0.125, ws.data_ptr(), nws, s) == cvattn.OK
 
-    ms, n = time_graph(torch, launch, 10, iters, 10)
+    ms, n = time_graph(torch, launch, 10, iters, 100)
     flops = 4.0 * D * B * HD * T * T
     return {"workload": "flow-DiT attention layer call, T=1500, batch 2, 16 heads, fp32 q/k/v views, single call",
             "us_per_layer_call": ms * 1e3, "tflops": flops / (ms * 1e-3) / 1e12, "workspace_bytes": nws, "calls": n}
 
 
-def bench_prefill(lib, cvattn, torch, dev, iters=48):
+def bench_prefill(lib, cvattn, torch, dev, iters=240):
     """LLM prefill layer call: 1024 query tokens over 1024 f16 cached tokens, causal mask, 14/2 heads
     (Q, K, V ~ 0.5 N(0,1)); 24 layers of the same shape are cycled."""
     nq = nkv = 1024
