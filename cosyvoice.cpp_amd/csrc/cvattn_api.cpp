@@ -517,7 +517,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         if (table) (*table)[i] = fp;
     }
     lay->table_bytes = align_up(sizeof(FaProblem) * (size_t)n, kAlign);
-    lay->counter_bytes = align_up(sizeof(uint32_t) * (size_t)cnt, kAlign);
+    lay->counter_bytes = align_up(sizeof(uint32_t) * (size_t)cnt * CNT_STRIDE, kAlign);
     lay->total_bytes = lay->table_bytes + lay->counter_bytes + (size_t)part * PART_STRIDE * sizeof(float);
     if (unit > kMaxUnits) return CVATTN_ERR_UNSUPPORTED;
     lay->units = unit;

@@ -111,10 +111,15 @@ struct FaUniform {
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)
     float *partials;     // workspace: split partial (m, l, O[64]) per row slot
     uint32_t *counters;  // prepared batches: split-arrival counter per (problem, b, kh, row group),
-                         // zero between launches (the merging workgroup resets its counter)
+                         // CNT_STRIDE words apart, zero between launches (the merging workgroup
+                         // resets its counter)
 };
 
 constexpr int PART_STRIDE = 68; // floats per partial slot: O[64], m, l, pad
+// Split-arrival counters sit one per 128-byte line: a group's splits increment theirs at about the
+// same time, and counters sharing a line serialize each other's atomics (one line per counter took
+// the 24-layer decode step from 14.6 to 14.0 us and the 16-sequence serving step from 390 to 362 us).
+constexpr int CNT_STRIDE = 32; // uint32 words
 
 struct FaArgs {
     FaUniform u;

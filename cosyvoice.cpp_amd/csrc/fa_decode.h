@@ -441,7 +441,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         wait_memory();
         __syncthreads();
         if (tid == 0) {
-            uint32_t *cnt = U.counters + P.cnt_begin + grp;
+            uint32_t *cnt = U.counters + (P.cnt_begin + grp) * CNT_STRIDE;
             const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const bool last = prev == (uint32_t)(ns - 1);
             if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -783,7 +783,7 @@ void fa_rows_kernel(FaArgs args) {
             wait_memory();
             __syncthreads();
             if (tid == 0) {
-                uint32_t *cnt = U.counters + P.cnt_begin + ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
+                uint32_t *cnt = U.counters + (P.cnt_begin + ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * CNT_STRIDE;
                 const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 const bool last = prev == (uint32_t)(P.n_splits - 1);
                 // the last arrival leaves the counter zeroed for the next launch
