@@ -57,9 +57,10 @@ __device__ __forceinline__ bool dec_row(const FaUniform &U, int kh, int rg, int 
     return ok;
 }
 
-// Split partials of one (batch, kv head, row group): O[16 row slots][ns][64] followed by
-// (m, l)[16 row slots][nsp][2] with nsp = ns rounded up to even (16-byte rows); this fits in the
-// 16 * ns * PART_STRIDE floats the host reserves per group.
+// Split partials of one (batch, kv head, row group): O[ns][16 row slots][64] (a split's rows are
+// one contiguous store run, and a merge load of one split covers 16 consecutive 256-byte rows)
+// followed by (m, l)[16 row slots][nsp][2] with nsp = ns rounded up to even (16-byte rows); this
+// fits in the 16 * ns * PART_STRIDE floats the host reserves per group.
 __device__ __forceinline__ int dec_ml_offset(int ns) { return 16 * ns * 64; }
 __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 
@@ -91,7 +92,7 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
 #pragma unroll
         for (int j = 0; j < DEC_MERGE_CHUNK; j++)
             ov[j] = __builtin_amdgcn_raw_buffer_load_b128(
-                rp, ok && c0 + j < ns ? ((r * ns + c0 + j) * 64 + d0) * 4 : kOutside, 0, AUX);
+                rp, ok && c0 + j < ns ? (((c0 + j) * 16 + r) * 64 + d0) * 4 : kOutside, 0, AUX);
 #pragma unroll
         for (int j = 0; j < DEC_MERGE_CHUNK / 2; j++)
             ml[j] = __builtin_amdgcn_raw_buffer_load_b128(
@@ -419,7 +420,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         return;
     }
     float *part0 = U.partials + slot0 * PART_STRIDE;
-    const int o_off = ((col * ns + split) * 64 + 16 * wv + 4 * g) * 4;
+    const int o_off = ((split * 16 + col) * 64 + 16 * wv + 4 * g) * 4;
     const int ml_off = (dec_ml_offset(ns) + (col * dec_nsp(ns) + split) * 2) * 4;
     if constexpr (!BATCH) {
         if (row_ok) {
