@@ -249,6 +249,25 @@ def test_dit_one_fp32_side(eng, orc, rng, kt, vt, cuda):
     run_case(eng, orc, c, what=f"dit k{kt} v{vt}")
 
 
+def test_dit_fp32_head_major_k_view(eng, orc, rng, cuda):
+    """fp32 K laid out head-major ([B][H][T][D]: nb1 = 256, nb2 = 256 T) and fp32 V token-major, an
+    odd T: the fp16 copies index both views through their own strides (row, head and batch
+    decomposition of the copy kernel)."""
+    T, B, H = 333, 2, 16
+    c = Case()
+    q = rng.standard_normal((B, T, H * D)).astype(np.float32)
+    c.add("q", q, F32, [D, T, H, B], [4, 4 * H * D, 4 * D, 4 * H * D * T])
+    k = rng.standard_normal((B, H, T, D)).astype(np.float32)
+    c.add("k", k, F32, [D, T, H, B], [4, 4 * D, 4 * D * T, 4 * D * T * H])
+    v = rng.standard_normal((B, T, H * D)).astype(np.float32)
+    c.add("v", v, F32, [D, T, H, B], [4, 4 * H * D, 4 * D, 4 * H * D * T])
+    c.mask_h = c.mask_d = None
+    c.out_shape = (B, T, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, T, B)
+    run_case(eng, orc, c, what="dit head-major fp32 K")
+
+
 def test_dit_chunk_mask(eng, orc, rng, cuda):
     T = 250
     mask = orc.chunk_mask(T, [50, 100, 150, 200])
