@@ -131,8 +131,10 @@ int check_dst(const cvattn_tensor *dst, const FaShape &sh) {
 }
 
 // Token splits.  Decode-shaped problems (waves split the tokens) size each wave's token run so
-// the whole launch has about kTargetWaves waves in flight (half that when each kv head has
-// several row groups, which already multiply the workgroups reading a head); row-tiled problems
+// the whole launch has about kTargetWaves waves in flight (an eighth of that when each kv head
+// has several row groups, which already multiply the workgroups reading a head: the 50-row DiT
+// chunk over 1050 tokens then runs unsplit, 10.2 us against 11.2 us with 3 splits at a half and
+// 10.75 us with 2 at a quarter); row-tiled problems
 // split only when their row groups alone cannot fill the chip.  `work` is the launch-wide sum
 // of B*H_kv*n_rowgroups*n_kv (decode) or of B*H_kv*n_rowgroups (row-tiled).
 constexpr int64_t kTargetWaves = 4096;
@@ -147,7 +149,7 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
     int len;
     if (sh.ks.wsplit) {
         // tokens per wave: a multiple of the wave step
-        const int64_t tw = sh.n_rowgroups > 1 ? kTargetWaves / 2 : kTargetWaves;
+        const int64_t tw = sh.n_rowgroups > 1 ? kTargetWaves / 8 : kTargetWaves;
         int64_t wlen = (std::max<int64_t>(1, work) + tw - 1) / tw;
         wlen = std::min<int64_t>(1024, std::max<int64_t>(tstep, (wlen + tstep - 1) / tstep * tstep));
         len = (int)wlen * sh.ks.nw;
