@@ -153,6 +153,24 @@ def test_decode_head_grouping(eng, orc, rng, H, Hkv, nq, B, kB, cuda):
         run_case(eng, orc, c, what=f"H {H} Hkv {Hkv} nq {nq} B {B} k{kt} v{vt}")
 
 
+def test_several_row_groups_over_long_cache_split(eng, orc, rng, cuda):
+    """50 query rows per kv head (four 16-row groups, as a DiT streaming chunk) over 9000 cached
+    f16 tokens: the decode kernel with several row groups and token splits merged in-kernel."""
+    c = llm_case(orc, rng, H=16, Hkv=16, nq=50, nkv=9000, kt=F16, vt=F16, max_seq=9000)
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.dst = c.q_d, c.k_d, c.v_d, c.dst_d
+    ws = workspace(eng.fa_batch_workspace([p]))
+    rc, plan = eng.fa_batch_prepare([p], 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+    check_close(host(c.dst), want, what="50 rows x 9000 tokens, batch")
+    single = empty_f32(*c.out_shape)
+    run_fa(eng, c.q_d, c.k_d, c.v_d, None, cvattn.out_view(single.data_ptr(), D, 16, 50))
+    check_close(host(single), want, what="50 rows x 9000 tokens, single call")
+
+
 def test_decode_two_query_tokens(eng, orc, rng, cuda):
     c = llm_case(orc, rng, nq=2, nkv=700, kt=Q8_0, vt=Q4_0, max_seq=1024)
     run_case(eng, orc, c, what="nq 2")
