@@ -189,7 +189,10 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 // range, this halves the chain each wave runs.
 template <int KT, int VT, bool MASK, bool BATCH, int KH>
 __global__ __launch_bounds__(64 * ROWS_NW * KH)
-__attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 ? 3 : 1))) // 3 per SIMD: 168 VGPRs
+// f16 K/V without mask: 3 waves per SIMD (168 VGPRs).  The masked instance does not fit 168 (it
+// spilled 104-108 bytes per lane there) and runs faster unconstrained (DiT T=1500 with a 50-frame
+// chunk mask: 73.3 -> 71.0 us).
+__attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 && !MASK ? 3 : 1)))
 void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int TSS = TS * KH; // tokens per staged step
