@@ -424,6 +424,9 @@ void fa_rows_kernel(FaArgs args) {
     // tokens t0..t0+TS), leaving its P^T operands in pb; `full_c` (std::true_type) says every
     // token of the tile is in range, so no bounds code is emitted (t0: this wave's 64 tokens, key
     // half hk of the staged step).  False when the mask removes the whole tile for this wave.
+    // mask words of this wave's next full tile, loaded one step ahead (mpre_t0: their first token)
+    u2 mpre[NR][NTILE];
+    int mpre_t0 = -1;
     auto qk_soft = [&](int kb, int vb, int t0, auto full_c) -> bool {
         const _Float16 *cK = sK[kb] + hk * TS * RSK;
         auto cS = [&](int x, int b) { return x < 2 ? &sSK[kb][x][b][hk * TS] : &sSV[vb][x - 2][b][hk * TS]; };
@@ -434,11 +437,31 @@ void fa_rows_kernel(FaArgs args) {
         if constexpr (MASK) {
             if constexpr (full) {
                 bool live = false;
+                if (mpre_t0 == t0) { // uniform
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+#pragma unroll
+                        for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = mpre[r][tt];
+                } else {
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+#pragma unroll
+                        for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
+                }
+                const int tn = t0 + TSS; // this wave's tile of the next step
+                if (tn + TS <= t_end) {  // uniform
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+#pragma unroll
+                        for (int tt = 0; tt < NTILE; tt++) mpre[r][tt] = ldg_u64(mrow[r] + (int64_t)(tn + 16 * tt + 4 * g) * 2);
+                    mpre_t0 = tn;
+                } else {
+                    mpre_t0 = -1;
+                }
 #pragma unroll
                 for (int r = 0; r < NR; r++)
 #pragma unroll
                     for (int tt = 0; tt < NTILE; tt++) {
-                        mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
                         // fp16 -inf is 0xfc00; any other half of the four keeps the tile
                         live |= row_ok[r] && ((mwv[r][tt][0] & 0xffffu) != 0xfc00u || (mwv[r][tt][0] >> 16) != 0xfc00u ||
                                               (mwv[r][tt][1] & 0xffffu) != 0xfc00u || (mwv[r][tt][1] >> 16) != 0xfc00u);
