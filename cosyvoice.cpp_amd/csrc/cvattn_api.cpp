@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstring>
 #include <limits>
@@ -21,17 +22,18 @@ namespace {
 constexpr int kRowsPerCu = 3;   // resident row-tiled workgroups per CU (register bound)
 constexpr int kDecodePerCu = 3; // resident decode workgroups per CU (41 KB of LDS each)
 
-// Compute units of the current device (256 on MI355X), cached per device.
+// Compute units of the current device (256 on MI355X).  The attribute is a fixed property of the
+// device, so it is read once per device; concurrent first calls store the same value.
 int cu_count() {
-    static int cached[64] = {0};
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (cached[dev] == 0) {
-        int n = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n == 0) {
         if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-        cached[dev] = n;
+        cached[dev].store(n, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return n;
 }
 constexpr size_t kAlign = 256;
 
@@ -108,11 +110,13 @@ int check_fa(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_tensor
     sh->B = (int)q->ne[3];
     sh->n_kv = (int)k->ne[1];
     sh->n_rows = sh->n_q * sh->G;
-    // 32-bit buffer offsets cover the rows of one K/V head a decode workgroup reads
+    // Both kernels address the K/V rows of one head with 32-bit buffer offsets (token * nb1): a
+    // view whose head spans 2^31 bytes or more is not served (the transposed V checks its own
+    // extent in vt_ok)
     const int64_t lim31 = ((int64_t)1 << 31) - 1;
-    const bool small = (int64_t)k->ne[1] * (int64_t)k->nb[1] < lim31 &&
-                       (vt || (int64_t)v->ne[1] * (int64_t)v->nb[1] < lim31);
-    sh->ks = fa_shape(sh->n_rows, small && !vt);
+    if ((int64_t)k->ne[1] * (int64_t)k->nb[1] >= lim31) return CVATTN_ERR_UNSUPPORTED;
+    if (!vt && (int64_t)v->ne[1] * (int64_t)v->nb[1] >= lim31) return CVATTN_ERR_UNSUPPORTED;
+    sh->ks = fa_shape(sh->n_rows, !vt);
     sh->n_rowgroups = (sh->n_rows + sh->ks.rows_per_group - 1) / sh->ks.rows_per_group;
     return CVATTN_OK;
 }
@@ -296,8 +300,9 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
     const bool many = !sh.ks.wsplit && sh.n_rowgroups >= kCvtMinRowGroups;
     // the transposed V's rows are its tokens: padded to 8 halfs, so they stay 16-byte aligned
     const int64_t v_row = vt ? (v->ne[0] + 7) / 8 * 8 : HEAD;
-    pl->cvt_k = many && k->type == T_F32 && view_rows(k) * (HEAD / 8) <= kCvtMaxChunks;
-    pl->cvt_v = many && v->type == T_F32 && view_rows(v) * (v_row / 8) <= kCvtMaxChunks;
+    // (an empty view -- n_kv 0 -- has nothing to copy)
+    pl->cvt_k = many && k->type == T_F32 && view_rows(k) > 0 && view_rows(k) * (HEAD / 8) <= kCvtMaxChunks;
+    pl->cvt_v = many && v->type == T_F32 && view_rows(v) > 0 && view_rows(v) * (v_row / 8) <= kCvtMaxChunks;
     pl->k_off = pl->v_off = 0;
     pl->v_row = 0;
     if (pl->cvt_k) {
@@ -453,8 +458,10 @@ struct BatchLayout {
     int64_t units, rows;
 };
 
+// n_kv_dev: plans whose n_kv is read from device memory at each launch (problem i reads
+// n_kv_dev[i * n_kv_stride]); the views' ne[1] is then the capacity the splits are planned for.
 static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProblem> *table, FaShape *sh0,
-                      BatchLayout *lay) {
+                      BatchLayout *lay, const int32_t *n_kv_dev = nullptr, int n_kv_stride = 0) {
     if (!probs || n <= 0) return CVATTN_ERR_BAD_ARGS;
     const bool has_mask = probs[0].mask.data != nullptr;
     int rc = check_fa(&probs[0].q, &probs[0].k, &probs[0].v, has_mask ? &probs[0].mask : nullptr, sh0);
@@ -505,6 +512,10 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         fp.n_splits = ns;
         fp.div_splits = make_fastdiv((uint32_t)ns);
         fp.split_len = sl;
+        if (n_kv_dev) {
+            fp.n_kv_dev = n_kv_dev + (int64_t)i * n_kv_stride;
+            fp.split_unit = sh.ks.wsplit ? sh.ks.tstep * sh.ks.nw : sh.ks.tstep * sh0->ks.kh;
+        }
         fp.unit_begin = unit;
         fp.part_begin = part;
         fp.row_begin = row;
@@ -534,14 +545,13 @@ CVATTN_API size_t cvattn_fa_batch_workspace(const cvattn_fa_problem *problems, i
     return lay.total_bytes;
 }
 
-CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n, float scale,
-                                       void *ws, size_t ws_bytes, cvattn_stream_t stream,
-                                       cvattn_fa_plan *plan) {
+static int prepare_batch(const cvattn_fa_problem *problems, int n, float scale, const int32_t *n_kv_dev,
+                         int n_kv_stride, void *ws, size_t ws_bytes, cvattn_stream_t stream, cvattn_fa_plan *plan) {
     if (!plan || !std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
     std::vector<FaProblem> table;
     FaShape sh;
     BatchLayout lay;
-    int rc = plan_batch(problems, n, &table, &sh, &lay);
+    int rc = plan_batch(problems, n, &table, &sh, &lay, n_kv_dev, n_kv_stride);
     if (rc) return rc;
     if (!ws || ws_bytes < lay.total_bytes) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
     BatchPlan bp;
@@ -575,6 +585,25 @@ CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n,
     std::memset(plan, 0, sizeof(*plan));
     std::memcpy(plan, &bp, sizeof(bp));
     return CVATTN_OK;
+}
+
+CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n, float scale,
+                                       void *ws, size_t ws_bytes, cvattn_stream_t stream,
+                                       cvattn_fa_plan *plan) {
+    return prepare_batch(problems, n, scale, nullptr, 0, ws, ws_bytes, stream, plan);
+}
+
+CVATTN_API int cvattn_fa_batch_prepare_dynamic(const cvattn_fa_problem *problems, int n, float scale,
+                                               const int32_t *n_kv_dev, int n_kv_stride, void *ws,
+                                               size_t ws_bytes, cvattn_stream_t stream, cvattn_fa_plan *plan) {
+    if (!n_kv_dev || (n_kv_stride != 0 && n_kv_stride != 1)) return CVATTN_ERR_BAD_ARGS;
+    if (((uintptr_t)n_kv_dev & 3) != 0) return CVATTN_ERR_BAD_ARGS;
+    return prepare_batch(problems, n, scale, n_kv_dev, n_kv_stride, ws, ws_bytes, stream, plan);
+}
+
+CVATTN_API int cvattn_shift_n_kv(int32_t *n_kv_dev, int n, int32_t delta, cvattn_stream_t stream) {
+    if (n < 0 || (n > 0 && !n_kv_dev) || ((uintptr_t)n_kv_dev & 3) != 0) return CVATTN_ERR_BAD_ARGS;
+    return hip_status(shift_n_kv_launch(n_kv_dev, n, delta, (hipStream_t)stream));
 }
 
 CVATTN_API int cvattn_fa_batch_launch(const cvattn_fa_plan *plan, cvattn_stream_t stream) {

@@ -92,6 +92,11 @@ struct FaProblem {
     int64_t row_begin;    // first output row (b, i, h) of this problem (combine indexing)
     int64_t cnt_begin;    // first split-arrival counter of this problem (prepared batches)
     FastDiv div_splits;   // n_splits
+    // Plans prepared with a device-resident n_kv (cvattn_fa_batch_prepare_dynamic): each launch
+    // reads n_kv here, n_kv above holds the capacity the plan was made for, and the launch spreads
+    // the tokens over the planned splits in runs of a multiple of split_unit tokens.
+    const int32_t *n_kv_dev;
+    int32_t split_unit;
 };
 
 // Parameters shared by every problem of one launch.

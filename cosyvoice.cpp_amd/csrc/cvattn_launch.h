@@ -20,7 +20,7 @@ struct FaKernelShape {
     int kh;             // row-tiled: key halves per workgroup (1, or 2 for launches with fewer row
                         // groups than CUs: 8 waves, two per row set, 128-token steps)
 };
-FaKernelShape fa_shape(int n_rows, bool small_views);
+FaKernelShape fa_shape(int n_rows, bool decode_ok);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
 // Row-tiled attention over a transposed V (vtype T_VT_F32 / T_VT_F16), single calls.
@@ -92,6 +92,7 @@ struct ChunkMaskArgs {
 };
 hipError_t chunk_mask_launch(const ChunkMaskArgs &a, hipStream_t st);
 hipError_t fill_positions_launch(int32_t *pos, int64_t n, int64_t batch, int64_t nb1, int32_t base, hipStream_t st);
+hipError_t shift_n_kv_launch(int32_t *n_kv, int32_t n, int32_t delta, hipStream_t st);
 hipError_t v_idxs_launch(int32_t *idx, const int32_t *pos, uint32_t n_tokens, uint32_t n_per_batch, uint32_t n_embd,
                          uint32_t max_seq, hipStream_t st);
 

@@ -139,6 +139,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     // one XCD so each line is fetched into one L2 only
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
     const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
+    resolve_n_kv<BATCH>(P);
 
     // the wave index is uniform per wave: readfirstlane lets the token range, step loop and
     // buffer soffsets live in scalar registers

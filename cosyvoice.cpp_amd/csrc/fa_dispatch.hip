@@ -23,12 +23,12 @@ static int type_index(int t) {
     }
 }
 
-FaKernelShape fa_shape(int n_rows, bool small_views) {
+FaKernelShape fa_shape(int n_rows, bool decode_ok) {
     FaKernelShape s;
     // decode-shaped kernel (fa_decode.h): <= 64 rows per kv head (up to 4 groups of 16, e.g. the
-    // 50 rows of a DiT streaming chunk) and K/V views addressable with 32-bit buffer offsets;
-    // everything else runs the row-tiled kernel
-    s.wsplit = n_rows <= 64 && small_views;
+    // 50 rows of a DiT streaming chunk), unless the caller rules it out (the transposed V of the
+    // non-flash-attention path); everything else runs the row-tiled kernel
+    s.wsplit = n_rows <= 64 && decode_ok;
     s.nw = 4;
     s.tstep = s.wsplit ? 32 : ROWS_TS;
     s.rows_per_group = s.wsplit ? 16 : ROWS_ROWS;

@@ -114,6 +114,26 @@ __device__ __forceinline__ UnitPos locate_unit(const FaArgs &args, uint32_t unit
     return r;
 }
 
+// A prepared plan with a device-resident n_kv: the launch reads the current length (clamped to
+// the capacity P.n_kv the plan was made for) and spreads it over the planned splits, each a
+// multiple of split_unit tokens; splits past the end run empty and merge with weight 0.  The
+// value is written before the launch (a kernel earlier on the stream, or a copy), so a plain
+// load sees it.
+template <bool BATCH>
+__device__ __forceinline__ void resolve_n_kv(FaProblem &P) {
+    if constexpr (BATCH) {
+        if (P.n_kv_dev != nullptr) {
+            // integer division runs on the VALU: the results go back to scalar registers, or every
+            // bound derived from them (token range, step count, buffer extents) would occupy VGPRs
+            const int n = min(max(*P.n_kv_dev, 0), P.n_kv);
+            const int per = (n + P.n_splits - 1) / P.n_splits;
+            const int u = P.split_unit;
+            P.split_len = __builtin_amdgcn_readfirstlane(max(u, (per + u - 1) / u * u));
+            P.n_kv = __builtin_amdgcn_readfirstlane(n);
+        }
+    }
+}
+
 // Last-arriving workgroup of a split row group merges all split partials of its rows
 // (prepared batches: no separate combine launch).  The partials were written by other
 // workgroups of the same launch and are read with agent-coherent (sc1) vector loads: (1) every
@@ -215,6 +235,7 @@ void fa_rows_kernel(FaArgs args) {
     FaProblem P;
     const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
     const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
+    resolve_n_kv<BATCH>(P);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -358,9 +358,23 @@ __global__ __launch_bounds__(256) void v_idxs_kernel(int32_t *idx, const int32_t
     idx[gid] = base + (int32_t)(j * max_seq);
 }
 
+// n_kv[i] += delta for i < n: the device-side length update of plans prepared with a device n_kv
+// (the counterpart of shift_kv_node_pos, src/cosyvoice-kv-cache.cpp:398-408, inside a captured
+// graph).
+__global__ __launch_bounds__(256) void shift_n_kv_kernel(int32_t *n_kv, int32_t n, int32_t delta) {
+    const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
+    if (i < n) n_kv[i] += delta;
+}
+
 // ------------------------------------------------------------------------------------------
 // Host launchers.
 // ------------------------------------------------------------------------------------------
+hipError_t shift_n_kv_launch(int32_t *n_kv, int32_t n, int32_t delta, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(shift_n_kv_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, n_kv, n, delta);
+    return hipGetLastError();
+}
+
 hipError_t chunk_mask_launch(const ChunkMaskArgs &a, hipStream_t st) {
     if (a.n_rows <= 0 || a.n_cols <= 0) return hipSuccess;
     hipLaunchKernelGGL(chunk_mask_kernel, dim3((unsigned)a.n_rows), dim3(256), 0, st, a);

@@ -163,6 +163,11 @@ class Lib:
         L.cvattn_fa_batch_prepare.restype = ctypes.c_int
         L.cvattn_fa_batch_launch.argtypes = [ctypes.POINTER(FaPlan), vp]
         L.cvattn_fa_batch_launch.restype = ctypes.c_int
+        L.cvattn_fa_batch_prepare_dynamic.argtypes = [PP, ctypes.c_int, ctypes.c_float, vp, ctypes.c_int, vp, sz, vp,
+                                                      ctypes.POINTER(FaPlan)]
+        L.cvattn_fa_batch_prepare_dynamic.restype = ctypes.c_int
+        L.cvattn_shift_n_kv.argtypes = [vp, ctypes.c_int, ctypes.c_int32, vp]
+        L.cvattn_shift_n_kv.restype = ctypes.c_int
         L.cvattn_block_size.argtypes = [ctypes.c_int]
         L.cvattn_block_size.restype = ctypes.c_int64
         L.cvattn_type_size.argtypes = [ctypes.c_int]
@@ -253,6 +258,16 @@ class Lib:
     def fa_batch_launch(self, plan, stream=0) -> int:
         return int(self.L.cvattn_fa_batch_launch(ctypes.byref(plan), stream or None))
 
+    def fa_batch_prepare_dynamic(self, problems, scale, n_kv_dev, n_kv_stride, ws, ws_bytes, stream=0):
+        arr = (FaProblem * len(problems))(*problems)
+        plan = FaPlan()
+        rc = int(self.L.cvattn_fa_batch_prepare_dynamic(arr, len(problems), scale, n_kv_dev or None, n_kv_stride,
+                                                        ws or None, ws_bytes, stream or None, ctypes.byref(plan)))
+        return rc, plan
+
+    def shift_n_kv(self, n_kv_dev, n, delta, stream=0) -> int:
+        return int(self.L.cvattn_shift_n_kv(n_kv_dev or None, n, delta, stream or None))
+
     # -- formats / KV write --
     def block_size(self, t) -> int:
         return int(self.L.cvattn_block_size(t))
@@ -327,6 +342,7 @@ class Lib:
 EXPORTED = [
     "cvattn_supports_flash_attn_ext", "cvattn_flash_attn_ext_workspace", "cvattn_flash_attn_ext",
     "cvattn_fa_batch_workspace", "cvattn_fa_batch_prepare", "cvattn_fa_batch_launch",
+    "cvattn_fa_batch_prepare_dynamic", "cvattn_shift_n_kv",
     "cvattn_block_size", "cvattn_type_size", "cvattn_dequantize",
     "cvattn_supports_set_rows", "cvattn_set_rows", "cvattn_rope", "cvattn_rope_set_rows",
     "cvattn_supports_attn_nonfa", "cvattn_attn_nonfa_workspace", "cvattn_attn_nonfa",

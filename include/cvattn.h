@@ -134,6 +134,25 @@ CVATTN_API int cvattn_fa_batch_prepare(const cvattn_fa_problem *problems, int n,
                                        cvattn_fa_plan *plan);
 CVATTN_API int cvattn_fa_batch_launch(const cvattn_fa_plan *plan, cvattn_stream_t stream);
 
+/* A prepared batch whose KV lengths live in device memory and are read at every launch: the
+ * decode loop of src/cosyvoice-llm.cpp:216-222 reuses one graph and grows n_kv in place with
+ * shift_kv_node_pos (src/cosyvoice-kv-cache.cpp:398-408); here one captured HIP graph
+ * (cvattn_shift_n_kv + cvattn_fa_batch_launch) serves every token with no re-prepare and no
+ * host synchronisation.
+ *   n_kv_dev     device int32; problem i reads n_kv_dev[i * n_kv_stride] (stride 0: one length
+ *                shared by every problem, e.g. the 24 layers of one sequence; stride 1: one per
+ *                problem, e.g. serving sequences).  Values are clamped to [0, capacity].
+ *   problems     as for cvattn_fa_batch_prepare, with k/v ne[1] = the capacity (e.g. max_seq):
+ *                the token splits are planned for it and each launch spreads the current length
+ *                over them; a mask must cover the capacity.
+ * The workspace size is cvattn_fa_batch_workspace(problems, n). */
+CVATTN_API int cvattn_fa_batch_prepare_dynamic(const cvattn_fa_problem *problems, int n, float scale,
+                                               const int32_t *n_kv_dev, int n_kv_stride, void *ws,
+                                               size_t ws_bytes, cvattn_stream_t stream, cvattn_fa_plan *plan);
+/* n_kv_dev[i] += delta for i < n, as a kernel on `stream` (capturable): the in-graph length
+ * update of a dynamic plan. */
+CVATTN_API int cvattn_shift_n_kv(int32_t *n_kv_dev, int n, int32_t delta, cvattn_stream_t stream);
+
 /* --------------------------------------------------------------------------------------------
  * The non-flash-attention path (--llm-flash-attn 0 / --flow-flash-attn 0): the node sequence
  *   scores = mul_mat(K, Q) (prec F32) -> soft_max_ext(scores, mask, scale, 0)

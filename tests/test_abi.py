@@ -197,3 +197,53 @@ def test_nonfa_argument_checks(eng):
     vstr = cvattn.tensor(FAKE, F16, [n, 64, 2, 1], [4] + list(vt.nb)[1:])      # tokens not contiguous
     assert eng.attn_nonfa(q, k, vstr, None, dst, 0.125) == cvattn.ERR_BAD_ARGS
     assert eng.attn_nonfa(q, k, vt, None, dst, 0.125, 0, 0) == cvattn.ERR_WORKSPACE_TOO_SMALL
+
+
+def test_views_past_32_bit_offsets_are_refused(eng):
+    """Both attention kernels address one head's K/V rows with 32-bit byte offsets (token * nb1):
+    a view whose head spans 2^31 bytes or more is reported unsupported (so the host keeps its own
+    path) instead of being read through a clamped buffer range."""
+    n_kv = 600000
+    q = cvattn.dit_view(FAKE, 2000, 1)
+    big = cvattn.dit_view(FAKE, n_kv, 1)                        # fp32 rows: 600000 * 4096 B > 2^31
+    small = cvattn.dit_view(FAKE, n_kv, 1, ttype=cvattn.F16)    # fp16 rows: 600000 * 2048 B < 2^31
+    for k, v in ((big, small), (small, big), (big, big)):
+        assert not eng.supports_flash_attn_ext(q, k, v, None)
+        dst = cvattn.out_view(FAKE, 64, 16, 2000, 1)
+        assert eng.flash_attn_ext(q, k, v, None, dst, 0.125, FAKE, 1 << 40) == cvattn.ERR_UNSUPPORTED
+    assert eng.supports_flash_attn_ext(q, small, small, None)
+    # one decode row over the same long view (the decode kernel has the same bound)
+    q1 = cvattn.dit_view(FAKE, 1, 1)
+    assert not eng.supports_flash_attn_ext(q1, big, small, None)
+    # a prepared batch holding such a problem is refused as well
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.dst = q1, big, small, cvattn.out_view(FAKE, 64, 16, 1, 1)
+    assert eng.fa_batch_workspace([p]) == 0
+
+
+def test_fp32_views_with_no_keys_need_no_copy(eng):
+    """n_kv = 0 with fp32 K/V and many query row groups: nothing to copy to fp16, so no
+    workspace (the call itself writes zeros; see the GPU test of the same shape)."""
+    q = cvattn.dit_view(FAKE, 300, 2)
+    k = cvattn.dit_view(FAKE, 0, 2)
+    assert eng.supports_flash_attn_ext(q, k, k, None)
+    assert eng.flash_attn_ext_workspace(q, k, k, None) == 0
+
+
+def test_dynamic_plan_validation(eng):
+    q, k, v, dst = llm(n_kv=4096)
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.dst = q, k, v, dst
+    ws = eng.fa_batch_workspace([p])
+    assert ws > 0
+    rc, _ = eng.fa_batch_prepare_dynamic([p], 0.125, 0, 0, FAKE, ws)            # no device length
+    assert rc == cvattn.ERR_BAD_ARGS
+    rc, _ = eng.fa_batch_prepare_dynamic([p], 0.125, FAKE, 2, FAKE, ws)         # stride 0 or 1 only
+    assert rc == cvattn.ERR_BAD_ARGS
+    rc, _ = eng.fa_batch_prepare_dynamic([p], 0.125, FAKE + 2, 0, FAKE, ws)     # int32 alignment
+    assert rc == cvattn.ERR_BAD_ARGS
+    rc, _ = eng.fa_batch_prepare_dynamic([p], 0.125, FAKE, 0, FAKE, ws - 1)
+    assert rc == cvattn.ERR_WORKSPACE_TOO_SMALL
+    assert eng.shift_n_kv(0, 1, 1) == cvattn.ERR_BAD_ARGS
+    assert eng.shift_n_kv(FAKE, -1, 1) == cvattn.ERR_BAD_ARGS
+    assert eng.shift_n_kv(0, 0, 1) == cvattn.OK       # nothing to do, no launch

@@ -519,3 +519,121 @@ def test_prefill_1024_causal(eng, orc, cuda):
     mask = orc.causal_mask(1024, 1024)
     c = llm_case(orc, rng, nq=1024, nkv=1024, kt=F16, vt=F16, max_seq=1024, mask=mask, qscale=0.5, kvscale=0.5)
     run_case(eng, orc, c, what="1024-token causal prefill")
+
+
+# ------------------------------------------------------------------------------------------
+# the instances behind the benchmark's numbers, with more row groups than CUs (one key half)
+# ------------------------------------------------------------------------------------------
+def cu_count():
+    return torch.cuda.get_device_properties(0).multi_processor_count
+
+
+def row_groups(B, Hkv, n_rows, rows_per_group=64):
+    """Row-tiled workgroups of a problem before token splits: one per 64 query rows of a kv head."""
+    return B * Hkv * ((n_rows + rows_per_group - 1) // rows_per_group)
+
+
+def batch_of(eng, cases, launches=1):
+    probs = []
+    for c in cases:
+        p = cvattn.FaProblem()
+        p.q, p.k, p.v, p.dst = c.q_d, c.k_d, c.v_d, c.dst_d
+        if c.mask_d is not None:
+            p.mask = c.mask_d
+        probs.append(p)
+    ws = workspace(eng.fa_batch_workspace(probs))
+    rc, plan = eng.fa_batch_prepare(probs, 0.125, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK, eng.status_string(rc)
+    for _ in range(launches):
+        for c in cases:
+            c.dst.fill_(float("nan"))
+        assert eng.fa_batch_launch(plan) == cvattn.OK
+    torch.cuda.synchronize()
+    return ws
+
+
+def test_dit_t1500_f16_prepared_batch(eng, orc, cuda):
+    """The benchmark's DiT call: f16 q/k/v views, T=1500, batch 2, 16 heads, no mask, through a
+    prepared batch (the timed form).  768 row groups > the CU count: one key half per workgroup."""
+    assert row_groups(2, 16, 1500) > cu_count()
+    rng = np.random.default_rng(1500)
+    c = dit_case(orc, rng, T=1500, ttype=F16)
+    batch_of(eng, [c], launches=2)
+    want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+    check_close(host(c.dst), want, what="dit T=1500 f16 batch")
+
+
+def dit_chunk_bounds(T, chunk=50):
+    return list(range(chunk, T, chunk))
+
+
+def test_dit_t1500_chunk_mask_fp32_views(eng, orc, cuda):
+    """The uncached streaming DiT step after the first chunk (src/cosyvoice-token2wav.cpp:285-298):
+    fp32 q/k/v views as the flow graph passes them (src/cosyvoice-graph.cpp:370-377), T=1500, a
+    chunk boundary every 50 frames, one cvattn_flash_attn_ext call (fp16 copies of K/V, the masked
+    one-half kernel)."""
+    T = 1500
+    assert row_groups(2, 16, T) > cu_count()
+    rng = np.random.default_rng(1501)
+    mask = orc.chunk_mask(T, dit_chunk_bounds(T))
+    c = dit_case(orc, rng, T=T, mask=mask)
+    run_case(eng, orc, c, what="dit T=1500 chunk mask, fp32 views")
+
+
+def test_dit_t1500_chunk_mask_f16_prepared_batch(eng, orc, cuda):
+    """The same masked call with f16 q/k/v through a prepared batch, launched twice."""
+    T = 1500
+    rng = np.random.default_rng(1502)
+    mask = orc.chunk_mask(T, dit_chunk_bounds(T))
+    c = dit_case(orc, rng, T=T, mask=mask, ttype=F16)
+    batch_of(eng, [c], launches=2)
+    want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
+    check_close(host(c.dst), want, what="dit T=1500 chunk mask f16 batch")
+
+
+def test_dit_stream_chunk_prepared_batch(eng, orc, cuda):
+    """The benchmark's DiT streaming call through a prepared batch: a 50-frame chunk over 1000
+    cached f16 frames plus itself (n_kv 1050), batch 2, 16 heads."""
+    nq, nkv, H, B = 50, 1050, 16, 2
+    rng = np.random.default_rng(1050)
+    c = Case()
+    q = rng.standard_normal((B, nq, H * D)).astype(np.float32)
+    c.add("q", q, F32, [D, nq, H, B], [4, 4 * H * D, 4 * D, 4 * H * D * nq])
+    for name in ("k", "v"):
+        x = orc.f32_to_f16(rng.standard_normal((B, nkv, H * D)).astype(np.float32))
+        c.add(name, x, F16, [D, nkv, H, B], [2, 2 * H * D, 2 * D, 2 * H * D * nkv])
+    c.mask_h = c.mask_d = None
+    c.out_shape = (B, nq, H, D)
+    c.dst = empty_f32(*c.out_shape)
+    c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, nq, B)
+    batch_of(eng, [c], launches=2)
+    want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+    check_close(host(c.dst), want, what="dit stream 50x1050 batch")
+
+
+def test_masked_prefill_batch_one_key_half(eng, orc, cuda):
+    """Three 1024-token causal prefill problems in one prepared batch: 3 x 224 row groups > the CU
+    count, so the masked batch kernel runs with one key half and no splits; launched twice."""
+    assert 3 * row_groups(1, 2, 1024 * 7) > cu_count()
+    rng = np.random.default_rng(3072)
+    mask = orc.causal_mask(1024, 1024)
+    cases = [llm_case(orc, rng, nq=1024, nkv=1024, kt=F16, vt=F16, max_seq=1024, mask=mask, qscale=0.5, kvscale=0.5)
+             for _ in range(3)]
+    batch_of(eng, cases, launches=2)
+    for i, c in enumerate(cases):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"masked prefill batch, problem {i}")
+
+
+def test_fp32_views_with_no_keys(eng, orc, cuda):
+    """n_kv = 0 with fp32 K/V and 300 query rows per head (5 row groups): nothing to copy or read;
+    every output row is 0, as ggml gives a row with no visible key."""
+    T, B, H = 300, 2, 16
+    rng = np.random.default_rng(0)
+    q = dev(rng.standard_normal((B, T, H * D)).astype(np.float32))
+    kv = dev(np.zeros((B, 1, H * D), dtype=np.float32))
+    qd = cvattn.dit_view(q.data_ptr(), T, B)
+    kd = cvattn.dit_view(kv.data_ptr(), 0, B)
+    out = empty_f32(B, T, H, D)
+    ws = run_fa(eng, qd, kd, kd, None, cvattn.out_view(out.data_ptr(), D, H, T, B))
+    assert np.all(host(out) == 0.0)

@@ -9,6 +9,7 @@ import torch
 
 import cvattn
 from _gpu import dev, host
+from _ties import tie_cases
 from oracle.oracle import F16, F32, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, QUANT_TYPES, TYPE_BYTES, row_bytes
 
 pytestmark = pytest.mark.gpu
@@ -105,3 +106,23 @@ def test_set_rows_dit_batch_index(eng, orc, cuda):
     it = cvattn.contiguous(d_idx.data_ptr(), cvattn.I32, [T, B, 1, 1])
     assert eng.set_rows(dt, st, it) == cvattn.OK
     assert np.array_equal(host(d_cache), want)
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+def test_set_rows_exact_ties_known_codes(eng, t, cuda):
+    """The quantize-on-write on inputs that land exactly on rounding ties (|id| = 1), against the
+    codes written out by hand from each *_ref tie rule (tests/_ties.py), not against the oracle."""
+    cases = tie_cases()[t]
+    x = np.stack([c[0] for c in cases]).astype(np.float32)      # one 32-element row per case
+    want = np.stack([c[1] for c in cases])
+    n = x.shape[0]
+    cache = np.full((n + 3, TYPE_BYTES[t]), 0xA5, dtype=np.uint8)
+    idx = (np.arange(n, dtype=np.int32) * 2 + 1) % (n + 3)
+    d_cache, d_src, d_idx = dev(cache), dev(x), dev(idx)
+    dt = cvattn.contiguous(d_cache.data_ptr(), t, [32, n + 3, 1, 1])
+    st = cvattn.contiguous(d_src.data_ptr(), F32, [32, n, 1, 1])
+    it = cvattn.contiguous(d_idx.data_ptr(), cvattn.I32, [n, 1, 1, 1])
+    assert eng.set_rows(dt, st, it) == cvattn.OK
+    got = host(d_cache)
+    for i in range(n):
+        assert list(got[idx[i]]) == list(want[i]), (t, i)

@@ -11,6 +11,7 @@ import os
 import numpy as np
 import pytest
 
+from _ties import tie_cases, tie_q8_0_cpu_case
 from oracle.oracle import F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, QUANT_TYPES, TYPE_BYTES
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
@@ -118,6 +119,21 @@ def test_dequantize_hand_blocks(orc, t):
     assert len(b) == TYPE_BYTES[t]
     got = orc.dequantize(t, np.frombuffer(b, dtype=np.uint8), 32)
     assert np.array_equal(got, want.astype(np.float32))
+
+
+@pytest.mark.parametrize("t", QUANT_TYPES)
+def test_quantize_exact_ties_known_codes(orc, t):
+    """Inputs on exact rounding ties (|id| = 1): the codes of each *_ref tie rule, written out by
+    hand in tests/_ties.py.  The |x - deq| <= d/2 invariants below hold under any tie rule; these
+    do not (rint instead of roundf, or roundf instead of the +0.5 truncation, changes them)."""
+    for x, want in tie_cases()[t]:
+        got = orc.quantize_flat(t, x)
+        assert list(got) == list(want), (t, list(got), list(want))
+
+
+def test_cpu_q8_0_variant_ties_to_even(orc):
+    x, want = tie_q8_0_cpu_case()
+    assert list(orc.quantize_q8_0_cpu(x)) == list(want)
 
 
 # ------------------------------------------------------------------------------------------
