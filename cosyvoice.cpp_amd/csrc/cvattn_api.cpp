@@ -355,6 +355,28 @@ int hip_status(hipError_t e) { return e == hipSuccess ? CVATTN_OK : CVATTN_ERR_H
 
 } // namespace
 
+// Workspace of cvattn_flash_attn_ext_noalloc: one array per GPU the library runs on, held until
+// the process ends.  Host code never passes `scratch` itself to a kernel or a copy (on the host it
+// is only a stand-in for the device symbol): the device address comes from hipGetSymbolAddress,
+// once per device with that device current, and is kept per device below.
+constexpr size_t kNoallocScratchBytes = (size_t)CVATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kNoallocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void *> g_scratch_ptr[kMaxDevices];
+
+// Device address of this device's `scratch`, looked up on the first call on the device (concurrent
+// first calls look up the same address).  nullptr on failure.
+static void *noalloc_scratch() {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+    void *ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+    if (ptr) return ptr;
+    if (hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)) != hipSuccess || !ptr) return nullptr;
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    return ptr;
+}
+
 extern "C" {
 
 CVATTN_API int cvattn_supports_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
@@ -426,6 +448,26 @@ static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvat
         return hip_status(fa_launch_vt(k->type, v->type == T_F32 ? T_VT_F32 : T_VT_F16, has_mask, a,
                                        (hipStream_t)stream));
     return hip_status(fa_launch(pl.sh.ks, k->type, v->type, has_mask, false, a, (hipStream_t)stream));
+}
+
+// ---- the no-allocation variant ------------------------------------------------------------------
+
+CVATTN_API int cvattn_flash_attn_ext_noalloc(const cvattn_tensor *q, const cvattn_tensor *k,
+                                             const cvattn_tensor *v, const cvattn_tensor *mask,
+                                             const cvattn_tensor *dst, float scale, float max_bias,
+                                             float logit_softcap, int prec, cvattn_stream_t stream) {
+    if (max_bias != 0.0f || logit_softcap != 0.0f) return CVATTN_ERR_UNSUPPORTED;
+    if (prec != CVATTN_PREC_DEFAULT && prec != CVATTN_PREC_F32) return CVATTN_ERR_BAD_ARGS;
+    if (!std::isfinite(scale)) return CVATTN_ERR_BAD_ARGS;
+    SinglePlan pl;
+    int rc = plan_single(q, k, v, mask, &pl);
+    if (rc) return rc;
+    if (pl.ws_bytes > kNoallocScratchBytes) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
+    void *ws = noalloc_scratch();
+    if (!ws) return CVATTN_ERR_HIP;
+    // The kernels fully write every byte of the workspace they later read (split partials, fp16
+    // copies); nothing in it has to start at zero.
+    return run_single(q, k, v, mask, dst, scale, ws, kNoallocScratchBytes, stream, false);
 }
 
 // ---- the non-flash-attention node sequence ----------------------------------------------------

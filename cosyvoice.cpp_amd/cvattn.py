@@ -29,6 +29,7 @@ BLOCK = {F32: 1, F16: 1, Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32}
 TYPE_BYTES = {F32: 4, F16: 2, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34}
 
 OK, ERR_UNSUPPORTED, ERR_BAD_ARGS, ERR_WORKSPACE_TOO_SMALL, ERR_HIP = 0, 1, 2, 3, 4
+NOALLOC_SCRATCH_BYTES = 32 << 20  # CVATTN_NOALLOC_SCRATCH_BYTES
 ROPE_NORMAL, ROPE_NEOX = 0, 2  # CVATTN_ROPE_* (ggml rope modes)
 PREC_DEFAULT, PREC_F32 = 0, 10
 
@@ -156,6 +157,9 @@ class Lib:
         L.cvattn_flash_attn_ext.argtypes = [P, P, P, P, P, ctypes.c_float, ctypes.c_float, ctypes.c_float,
                                             ctypes.c_int, vp, sz, vp]
         L.cvattn_flash_attn_ext.restype = ctypes.c_int
+        L.cvattn_flash_attn_ext_noalloc.argtypes = [P, P, P, P, P, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                                                    ctypes.c_int, vp]
+        L.cvattn_flash_attn_ext_noalloc.restype = ctypes.c_int
         PP = ctypes.POINTER(FaProblem)
         L.cvattn_fa_batch_workspace.argtypes = [PP, ctypes.c_int]
         L.cvattn_fa_batch_workspace.restype = sz
@@ -243,6 +247,11 @@ class Lib:
         return int(self.L.cvattn_flash_attn_ext(self._p(q), self._p(k), self._p(v), self._p(mask), self._p(dst),
                                                 scale, max_bias, softcap, prec, ws or None, ws_bytes,
                                                 stream or None))
+
+    def flash_attn_ext_noalloc(self, q, k, v, mask, dst, scale, stream=0, max_bias=0.0, softcap=0.0,
+                               prec=PREC_F32) -> int:
+        return int(self.L.cvattn_flash_attn_ext_noalloc(self._p(q), self._p(k), self._p(v), self._p(mask),
+                                                        self._p(dst), scale, max_bias, softcap, prec, stream or None))
 
     def fa_batch_workspace(self, problems) -> int:
         arr = (FaProblem * len(problems))(*problems)
@@ -341,6 +350,7 @@ class Lib:
 
 EXPORTED = [
     "cvattn_supports_flash_attn_ext", "cvattn_flash_attn_ext_workspace", "cvattn_flash_attn_ext",
+    "cvattn_flash_attn_ext_noalloc",
     "cvattn_fa_batch_workspace", "cvattn_fa_batch_prepare", "cvattn_fa_batch_launch",
     "cvattn_fa_batch_prepare_dynamic", "cvattn_shift_n_kv",
     "cvattn_block_size", "cvattn_type_size", "cvattn_dequantize",

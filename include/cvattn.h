@@ -103,6 +103,20 @@ CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor
                                      float logit_softcap, int prec, void *ws, size_t ws_bytes,
                                      cvattn_stream_t stream);
 
+/* cvattn_flash_attn_ext without a caller workspace and without any allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate or pass scratch memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its workspace is a
+ * fixed array of CVATTN_NOALLOC_SCRATCH_BYTES in the library's device memory, one per GPU, held
+ * until the process ends; a call whose shapes need more (cvattn_flash_attn_ext_workspace) returns
+ * CVATTN_ERR_WORKSPACE_TOO_SMALL.  All calls on one GPU share that array: calls that overlap on
+ * one GPU (two streams, or two threads) race and must be serialised by the caller.  Otherwise it
+ * behaves exactly as cvattn_flash_attn_ext (same kernels, same results). */
+#define CVATTN_NOALLOC_SCRATCH_BYTES (32u << 20)
+CVATTN_API int cvattn_flash_attn_ext_noalloc(const cvattn_tensor *q, const cvattn_tensor *k,
+                                             const cvattn_tensor *v, const cvattn_tensor *mask,
+                                             const cvattn_tensor *dst, float scale, float max_bias,
+                                             float logit_softcap, int prec, cvattn_stream_t stream);
+
 /* --------------------------------------------------------------------------------------------
  * Batched flash attention: many independent ggml_flash_attn_ext problems in one launch.
  * cosyvoice.cpp runs one FA node per layer per worker (src/cosyvoice-llm.cpp:247-255,

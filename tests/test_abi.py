@@ -247,3 +247,14 @@ def test_dynamic_plan_validation(eng):
     assert eng.shift_n_kv(0, 1, 1) == cvattn.ERR_BAD_ARGS
     assert eng.shift_n_kv(FAKE, -1, 1) == cvattn.ERR_BAD_ARGS
     assert eng.shift_n_kv(0, 0, 1) == cvattn.OK       # nothing to do, no launch
+
+
+def test_noalloc_size_limit_checked_before_any_launch(eng):
+    """fp32 DiT views of 5000 frames need more than the fixed scratch array for their fp16 K/V
+    copies: refused with WORKSPACE_TOO_SMALL before anything touches the device."""
+    T, B = 5000, 2
+    qv = cvattn.dit_view(FAKE, T, B)
+    assert eng.flash_attn_ext_workspace(qv, qv, qv, None) > cvattn.NOALLOC_SCRATCH_BYTES
+    dst = cvattn.out_view(FAKE, 64, 16, T, B)
+    assert eng.flash_attn_ext_noalloc(qv, qv, qv, None, dst, 0.125) == cvattn.ERR_WORKSPACE_TOO_SMALL
+    assert eng.flash_attn_ext_noalloc(qv, qv, qv, None, dst, 0.125, max_bias=1.0) == cvattn.ERR_UNSUPPORTED
