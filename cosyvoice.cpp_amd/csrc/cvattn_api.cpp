@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <limits>
 #include <vector>
@@ -252,6 +253,60 @@ void fill_uniform(FaUniform &u, const FaShape &sh, int q_type, float scale) {
     u.div_upp = make_fastdiv(1);
 }
 
+// The preloaded addressing of a decode launch (DecPre) when its problems allow it: one sequence,
+// one query token and so one row group per kv head, no mask, a static n_kv, f32 Q with contiguous
+// heads, kv heads dense in the cache rows, row bytes and split lengths below 2^16, and problem
+// i's K, V and Q at i times a fixed int32 byte stride from problem 0's, all with the same n_kv and
+// split plan.  Leaves a.pre zeroed (the kernel then locates its problem in memory) otherwise.
+void fill_dec_pre(FaArgs &a, const FaShape &sh, const FaProblem *probs, int n, int q_type, bool has_mask) {
+    std::memset(&a.pre, 0, sizeof(a.pre));
+    if (!sh.ks.wsplit || has_mask || n < 1 || sh.B != 1 || sh.n_q != 1 || sh.n_rowgroups != 1) return;
+    if (q_type != T_F32 || sh.H_kv > 255 || sh.G > 255) return;
+    const FaProblem &p0 = probs[0];
+    if (p0.n_kv_dev || p0.q_nb2 != HEAD * 4) return;
+    for (const int64_t nb1_nb2 : {p0.k_nb1, p0.v_nb1})
+        if (nb1_nb2 <= 0 || nb1_nb2 >= 65536 || nb1_nb2 % sh.H_kv) return;
+    if (p0.k_nb2 * sh.H_kv != p0.k_nb1 || p0.v_nb2 * sh.H_kv != p0.v_nb1) return;
+    if (p0.split_len <= 0 || p0.split_len >= 65536 || p0.n_splits >= 256 || p0.n_kv >= (1 << 24)) return;
+    const int64_t k_ps = n > 1 ? (const uint8_t *)probs[1].k - (const uint8_t *)p0.k : 0;
+    const int64_t v_ps = n > 1 ? (const uint8_t *)probs[1].v - (const uint8_t *)p0.v : 0;
+    const int64_t q_ps = n > 1 ? (const uint8_t *)probs[1].q - (const uint8_t *)p0.q : 0;
+    for (const int64_t ps : {k_ps, v_ps, q_ps})
+        if (ps < INT32_MIN || ps > INT32_MAX) return;
+    // outputs at a uniform float stride, and the partial slots and counters the planner laid out
+    // problem after problem (H_kv groups each)
+    const int64_t dst_ps = n > 1 ? probs[1].dst - p0.dst : 0;
+    for (int i = 0; i < n; i++) {
+        const FaProblem &pi = probs[i];
+        if ((const uint8_t *)pi.k - (const uint8_t *)p0.k != i * k_ps ||
+            (const uint8_t *)pi.v - (const uint8_t *)p0.v != i * v_ps ||
+            (const uint8_t *)pi.q - (const uint8_t *)p0.q != i * q_ps)
+            return;
+        if (pi.dst - p0.dst != i * dst_ps) return;
+        const int64_t groups = (int64_t)sh.H_kv;
+        if (pi.part_begin != (p0.n_splits > 1 ? i * groups * 16 * p0.n_splits : 0) ||
+            (p0.n_splits > 1 && pi.cnt_begin != i * groups))
+            return;
+        if (pi.n_kv != p0.n_kv || pi.n_splits != p0.n_splits || pi.split_len != p0.split_len || pi.n_kv_dev ||
+            pi.k_nb1 != p0.k_nb1 || pi.v_nb1 != p0.v_nb1 || pi.k_nb2 != p0.k_nb2 || pi.v_nb2 != p0.v_nb2 ||
+            pi.q_nb2 != p0.q_nb2)
+            return;
+    }
+    DecPre &d = a.pre;
+    d.k = (const uint8_t *)p0.k;
+    d.v = (const uint8_t *)p0.v;
+    d.q = (const uint8_t *)p0.q;
+    d.k_ps = (int32_t)k_ps;
+    d.v_ps = (int32_t)v_ps;
+    d.q_ps = (int32_t)q_ps;
+    d.kv = (uint32_t)p0.n_kv | ((uint32_t)p0.n_splits << 24);
+    d.lens = (uint32_t)p0.split_len | ((uint32_t)p0.k_nb1 << 16);
+    d.shape = (uint32_t)p0.v_nb1 | ((uint32_t)sh.H_kv << 16) | ((uint32_t)sh.G << 24);
+    d.units = (uint32_t)a.u.total_units;
+    d.scale_log2 = a.u.scale_log2;
+    a.dst_ps = dst_ps;
+}
+
 // Workgroup units of a launch are decomposed with 32-bit arithmetic.
 constexpr int64_t kMaxUnits = ((int64_t)1 << 31) - 1;
 
@@ -444,6 +499,7 @@ static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvat
     a.u.total_rows = (int64_t)pl.sh.B * pl.sh.H * pl.sh.n_q;
     a.u.partials = (float *)ws;
     const bool has_mask = mask && mask->data;
+    if (!vt) fill_dec_pre(a, pl.sh, &a.p0, 1, q->type, has_mask);
     if (vt)
         return hip_status(fa_launch_vt(k->type, v->type == T_F32 ? T_VT_F32 : T_VT_F16, has_mask, a,
                                        (hipStream_t)stream));
@@ -618,6 +674,7 @@ static int prepare_batch(const cvattn_fa_problem *problems, int n, float scale, 
     bp.args.u.partials = (float *)((char *)ws + lay.table_bytes + lay.counter_bytes);
     bp.args.p0 = table[0];
     bp.args.table = (const FaProblem *)ws;
+    fill_dec_pre(bp.args, sh, table.data(), n, problems[0].q.type, bp.has_mask != 0);
     // one upload: the table followed by zeroed counters (the kernels keep them zero afterwards)
     std::vector<unsigned char> head(lay.table_bytes + lay.counter_bytes, 0);
     std::memcpy(head.data(), table.data(), sizeof(FaProblem) * (size_t)n);

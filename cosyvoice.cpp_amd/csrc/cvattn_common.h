@@ -126,10 +126,30 @@ constexpr int PART_STRIDE = 68; // floats per partial slot: O[64], m, l, pad
 // the 24-layer decode step from 14.6 to 14.0 us and the 16-sequence serving step from 390 to 362 us).
 constexpr int CNT_STRIDE = 32; // uint32 words
 
+// What a decode workgroup needs to address its K/V and Q loads, for launches whose problems are
+// laid out at uniform strides (the layers of one cache buffer, or a single problem) with one
+// sequence, one query token and one row group per kv head, no mask and f32 Q with contiguous
+// heads.  The decode kernel takes these 14 dwords as its leading arguments, which the dispatcher
+// preloads into scalar registers: a workgroup issues its loads and converts its Q without first
+// reading its kernel arguments or a problem table from memory, which, once the other workgroups'
+// K/V requests fill the memory queues, waits behind them.  G == 0: the kernel locates its problem
+// as before.
+struct DecPre {
+    const uint8_t *k, *v, *q;  // problem 0: K and V rows of kv head 0, the Q rows
+    int32_t k_ps, v_ps, q_ps;  // byte stride from one problem to the next
+    uint32_t kv;               // n_kv | n_splits << 24
+    uint32_t lens;             // split_len | K row bytes << 16 (kv head h at h * row / H_kv)
+    uint32_t shape;            // V row bytes | H_kv << 16 | G << 24 (G = 0: not preloaded)
+    uint32_t units;            // workgroups of the launch
+    float scale_log2;          // softmax scale * log2(e)
+};
+
 struct FaArgs {
     FaUniform u;
     FaProblem p0;              // used when n_problems == 1
     const FaProblem *table;    // device table when n_problems > 1
+    DecPre pre;                // decode launches: the preloaded addressing (pre.shape G field set)
+    int64_t dst_ps;            // with pre: float stride from one problem's output to the next
 };
 
 } // namespace cvattn

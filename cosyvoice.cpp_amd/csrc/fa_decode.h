@@ -71,8 +71,8 @@ __device__ __forceinline__ int dec_nsp(int ns) { return (ns + 1) & ~1; }
 // second round rescales the running sum to the new maximum.
 // SC1: the partials were written by other workgroups of the same launch (agent-coherent loads).
 template <bool SC1>
-__device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P, float *part0, int ns, int kh,
-                                          int rg, int bq) {
+__device__ __forceinline__ void dec_merge(const FaUniform &U, float *dst, float *part0, int ns, int kh, int rg,
+                                          int bq) {
     const int tid = threadIdx.x;
     const int r = tid >> 4, q = tid & 15, d0 = 4 * q;
     int iq, hq;
@@ -120,11 +120,19 @@ __device__ __forceinline__ void dec_merge(const FaUniform &U, const FaProblem &P
     }
     if (!ok) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    *(f4 *)&P.dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
+    *(f4 *)&dst[(((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD + d0] = acc * inv;
 }
 
+// The kernel's leading arguments are the DecPre words (cvattn_common.h), preloaded into scalar
+// registers at wave launch (the decode translation units are built with
+// -amdgpu-kernarg-preload-count=11); `args` is read from memory as usual.
 template <int KT, int VT, bool MASK, bool BATCH>
-__global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
+__global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(const uint8_t *pre_k, const uint8_t *pre_v,
+                                                                 const uint8_t *pre_q, int32_t pre_k_ps,
+                                                                 int32_t pre_v_ps, int32_t pre_q_ps, uint32_t pre_kv,
+                                                                 uint32_t pre_lens, uint32_t pre_shape,
+                                                                 uint32_t pre_units, float pre_scale_log2,
+                                                                 FaArgs args) {
     constexpr int TS = 32;                     // tokens per wave step
     constexpr int NT = 2;                      // 16-token score tiles per step
     constexpr int PD = dec_prefetch<KT, VT>(); // steps in flight
@@ -135,20 +143,78 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 
     const FaUniform &U = args.u;
     FaProblem P;
-    // consecutive units (the kv heads of one token range, whose rows share cache lines) run on
-    // one XCD so each line is fetched into one L2 only
-    const UnitPos pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
-    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
-    resolve_n_kv<BATCH>(P);
-
     // the wave index is uniform per wave: readfirstlane lets the token range, step loop and
     // buffer soffsets live in scalar registers
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15, g = lane >> 4;
 
-    const int t_begin = split * P.split_len;
-    const int t_end = min(P.n_kv, t_begin + P.split_len);
-    const int wlen = P.split_len / DEC_NW;
+    // ---- the workgroup's unit and the addressing of its loads ----
+    // Consecutive units (the kv heads of one token range, whose rows share cache lines) run on
+    // one XCD so each line is fetched into one L2 only.
+    UnitPos pos;
+    gu8 *kbase, *vbase;
+    int n_kv, split_len, k_nb1, v_nb1;
+    // the epilogue's view of the problem: output, split count, first partial slot and counter
+    float *dst = nullptr;
+    int ns;
+    int64_t part_begin, cnt_begin;
+    uint32_t fast_p = 0; // the problem index on the preloaded path
+    int iq, hq;
+    bool row_ok;
+    gu8 *qp;
+    const bool fast = !MASK && (pre_shape >> 24) != 0; // uniform
+    if (fast) {
+        // everything from the preloaded words: no memory access before the loads are issued
+        const uint32_t hkv = (pre_shape >> 16) & 0xffu, G = pre_shape >> 24;
+        const uint32_t upp = (pre_kv >> 24) * hkv; // units per problem: splits x kv heads
+        const uint32_t unit = xcd_unit(blockIdx.x, pre_units);
+        const uint32_t p = __builtin_amdgcn_readfirstlane(unit / upp);
+        const uint32_t ul = unit - p * upp;
+        const uint32_t sp = __builtin_amdgcn_readfirstlane(ul / hkv);
+        pos.kh = (int)(ul - sp * hkv);
+        pos.split = (int)sp;
+        pos.rg = 0;
+        pos.bq = 0;
+        k_nb1 = (int)(pre_lens >> 16);
+        v_nb1 = (int)(pre_shape & 0xffffu);
+        const int k_nb2 = __builtin_amdgcn_readfirstlane(k_nb1 / (int)hkv);
+        const int v_nb2 = __builtin_amdgcn_readfirstlane(v_nb1 / (int)hkv);
+        kbase = gptr(pre_k) + (int64_t)p * pre_k_ps + (int64_t)pos.kh * k_nb2;
+        vbase = gptr(pre_v) + (int64_t)p * pre_v_ps + (int64_t)pos.kh * v_nb2;
+        n_kv = (int)(pre_kv & 0xffffffu);
+        split_len = (int)(pre_lens & 0xffffu);
+        // one query token: row `col` of the kv head is q head kh*G + col, contiguous f32 heads
+        row_ok = col < (int)G;
+        iq = 0;
+        hq = pos.kh * (int)G + (row_ok ? col : 0);
+        qp = gptr(pre_q) + (int64_t)p * pre_q_ps + (int64_t)hq * (HEAD * 4);
+        // the problems of a uniform launch follow each other in the output, the partial slots and
+        // the arrival counters (H_kv groups of 16 row slots per problem)
+        ns = (int)(pre_kv >> 24);
+        fast_p = p; // the output pointer comes from the kernel arguments, in the epilogue
+        part_begin = ns > 1 ? (int64_t)p * hkv * 16 * ns : 0;
+        cnt_begin = (int64_t)p * hkv;
+    } else {
+        pos = locate_unit<BATCH>(args, xcd_unit(blockIdx.x, gridDim.x), P);
+        resolve_n_kv<BATCH>(P);
+        kbase = gptr(P.k) + (int64_t)pos.kh * P.k_nb2 + (int64_t)(pos.bq / P.rk3) * P.k_nb3;
+        vbase = gptr(P.v) + (int64_t)pos.kh * P.v_nb2 + (int64_t)(pos.bq / P.rv3) * P.v_nb3;
+        n_kv = P.n_kv;
+        split_len = P.split_len;
+        k_nb1 = (int)P.k_nb1;
+        v_nb1 = (int)P.v_nb1;
+        row_ok = dec_row(U, pos.kh, pos.rg, col, iq, hq);
+        qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)pos.bq * P.q_nb3;
+        dst = P.dst;
+        ns = P.n_splits;
+        part_begin = P.part_begin;
+        cnt_begin = P.cnt_begin;
+    }
+    const int kh = pos.kh, rg = pos.rg, split = pos.split, bq = pos.bq;
+
+    const int t_begin = split * split_len;
+    const int t_end = min(n_kv, t_begin + split_len);
+    const int wlen = split_len / DEC_NW;
     const int w_begin = t_begin + wv * wlen;
     const int w_end = min(t_end, w_begin + wlen);
     const int nsteps = (max(0, w_end - w_begin) + TS - 1) / TS; // per wave
@@ -157,54 +223,66 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
     const int lt = lane >> 1;
     const int lb = lane & 1;
     const int lrow = lt;
-    gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
-    gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
     // the head rows this workgroup reads: loads of tokens >= n_kv fall outside and read 0
-    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
-    const int64_t vext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>() : 0;
+    const int64_t kext = n_kv > 0 ? (int64_t)(n_kv - 1) * k_nb1 + 2 * dblk_bytes<KT>() : 0;
+    const int64_t vext = n_kv > 0 ? (int64_t)(n_kv - 1) * v_nb1 + 2 * dblk_bytes<VT>() : 0;
     const __amdgpu_buffer_rsrc_t rk = make_rsrc(kbase, kext);
     const __amdgpu_buffer_rsrc_t rv = make_rsrc(vbase, vext);
-    const int kvoff = lt * (int)P.k_nb1 + lb * dblk_bytes<KT>();
-    const int vvoff = lt * (int)P.v_nb1 + lb * dblk_bytes<VT>();
+    const int kvoff = lt * k_nb1 + lb * dblk_bytes<KT>();
+    const int vvoff = lt * v_nb1 + lb * dblk_bytes<VT>();
 
     // ---- this lane's query row (MFMA column `col`) and its Q operand (hi + lo fp16) ----
-    int iq, hq;
-    const bool row_ok = dec_row(U, kh, rg, col, iq, hq);
     h8 qhi[2], qlo[2];
     float qsum[2];
     bool need_lo = false;
     RawBuf<blk_words<KT>()> RK[PD];
     RawBuf<blk_words<VT>()> RV[PD];
     {
-        gu8 *qp = gptr(P.q) + (int64_t)iq * P.q_nb1 + (int64_t)hq * P.q_nb2 + (int64_t)bq * P.q_nb3;
         float x[2][8];
-        if (U.q_f16) {
+        // The K/V loads go out right behind Q, so the Q conversion below overlaps their latency
+        // (memory results return in issue order).  They are issued for every prefetch step: a
+        // step this wave does not have reads at an offset past the resource, which returns 0
+        // without a memory access, so the load count is fixed and the Q conversion waits for Q
+        // alone.
+        constexpr int kPast = 0x40000000;
+        auto issue_kv = [&]() {
 #pragma unroll
-            for (int b = 0; b < 2; b++)
-#pragma unroll
-                for (int j = 0; j < 8; j++) x[b][j] = ldg_half(qp + 2 * (32 * b + 8 * g + j));
-        } else {
+            for (int p = 0; p < PD; p++) {
+                blk_load<KT>(rk, kvoff, p < nsteps ? (w_begin + p * TS) * k_nb1 : kPast, RK[p]);
+                blk_load<VT>(rv, vvoff, p < nsteps ? (w_begin + p * TS) * v_nb1 : kPast, RV[p]);
+            }
+        };
+        auto load_q32 = [&]() {
 #pragma unroll
             for (int b = 0; b < 2; b++)
 #pragma unroll
                 for (int j = 0; j < 8; j++) x[b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
-        }
-        // the K/V loads go out right behind Q, so the Q conversion below overlaps their latency
-        // (memory results return in issue order)
+        };
+        if (fast) {
+            // nothing read from memory yet: f32 Q, then K/V
+            load_q32();
+            issue_kv();
+        } else {
+            if (U.q_f16) {
 #pragma unroll
-        for (int p = 0; p < PD; p++) {
-            if (p < nsteps) {
-                blk_load<KT>(rk, kvoff, (w_begin + p * TS) * (int)P.k_nb1, RK[p]);
-                blk_load<VT>(rv, vvoff, (w_begin + p * TS) * (int)P.v_nb1, RV[p]);
+                for (int b = 0; b < 2; b++)
+#pragma unroll
+                    for (int j = 0; j < 8; j++) x[b][j] = ldg_half(qp + 2 * (32 * b + 8 * g + j));
+            } else {
+                load_q32();
             }
+            issue_kv();
         }
+        // keep every load above ahead of the Q conversion (the scheduler would otherwise sink
+        // them below it, behind the wait for Q)
+        __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
         for (int b = 0; b < 2; b++) {
             float s = 0.0f;
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const float xs = row_ok ? x[b][j] * U.scale_log2 : 0.0f;
+                const float xs = row_ok ? x[b][j] * (fast ? pre_scale_log2 : U.scale_log2) : 0.0f;
                 const _Float16 hx = (_Float16)xs;
                 const _Float16 lx = (_Float16)(xs - (float)hx);
                 qhi[b][j] = hx;
@@ -215,7 +293,9 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
             qsum[b] = wave_sum16x4(s);
         }
     }
-    need_lo = __syncthreads_or(need_lo) != 0;
+    // every wave holds the whole Q block, so the wave's own vote is the workgroup's (a workgroup
+    // vote would read the launch's group size from memory)
+    need_lo = __builtin_amdgcn_ballot_w64(need_lo) != 0;
     constexpr float kbias = stage_bias<KT>();
     const f4 cinit0 = {-kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0], -kbias * qsum[0]};
     const f4 cinit1 = {-kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1], -kbias * qsum[1]};
@@ -254,8 +334,8 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
                     if constexpr (has_min(VT)) tS[3][lb][lrow] = m;
                 }
                 if (step + PD < nsteps) {
-                    blk_load<KT>(rk, kvoff, (t0 + PD * TS) * (int)P.k_nb1, RK[p]);
-                    blk_load<VT>(rv, vvoff, (t0 + PD * TS) * (int)P.v_nb1, RV[p]);
+                    blk_load<KT>(rk, kvoff, (t0 + PD * TS) * k_nb1, RK[p]);
+                    blk_load<VT>(rv, vvoff, (t0 + PD * TS) * v_nb1, RV[p]);
                 }
                 // the tile is wave-private: LDS keeps one wave's accesses in order
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -309,7 +389,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
 #pragma unroll
                             for (int j = 0; j < 4; j++) {
                                 const int t = tb + j;
-                                const float mv = ldg_half(mrow + (int64_t)min(t, P.n_kv - 1) * 2);
+                                const float mv = ldg_half(mrow + (int64_t)min(t, n_kv - 1) * 2);
                                 sc[s][j] = t < w_end ? sc[s][j] + mv * 1.4426950408889634f : -INFINITY;
                             }
                         }
@@ -409,13 +489,13 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         for (int j = 0; j < 4; j++) o[j] += xo[(w * 64 + 16 * wv + 4 * g + j) * 16 + col] * f;
     }
     // wave wv now owns dims 16*wv + 4g + j of row slot `col`
-    const int ns = P.n_splits;
+    if (fast) dst = args.p0.dst + (int64_t)fast_p * args.dst_ps;
     const int64_t grp = ((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg;
-    const int64_t slot0 = P.part_begin + grp * 16 * ns;
+    const int64_t slot0 = part_begin + grp * 16 * ns;
     if (ns == 1) {
         if (row_ok) {
             const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-            float *out = P.dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
+            float *out = dst + (((int64_t)bq * U.n_q + iq) * U.H + hq) * HEAD;
             *(f4 *)&out[16 * wv + 4 * g] = o * inv;
         }
         return;
@@ -443,7 +523,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         wait_memory();
         __syncthreads();
         if (tid == 0) {
-            uint32_t *cnt = U.counters + (P.cnt_begin + grp) * CNT_STRIDE;
+            uint32_t *cnt = U.counters + (cnt_begin + grp) * CNT_STRIDE;
             const uint32_t prev = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const bool last = prev == (uint32_t)(ns - 1);
             if (last) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -451,7 +531,7 @@ __global__ __launch_bounds__(64 * DEC_NW) void fa_decode_kernel(FaArgs args) {
         }
         __syncthreads();
         if (!s_last) return;
-        dec_merge<true>(U, P, part0, ns, kh, rg, bq);
+        dec_merge<true>(U, dst, part0, ns, kh, rg, bq);
     }
 }
 
@@ -463,7 +543,7 @@ static __global__ __launch_bounds__(256) void dec_combine_kernel(FaArgs args) {
     const int rg = (int)(grp % U.n_rowgroups);
     const int kh = (int)((grp / U.n_rowgroups) % U.H_kv);
     const int bq = (int)(grp / ((int64_t)U.n_rowgroups * U.H_kv));
-    dec_merge<false>(U, P, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, kh,
+    dec_merge<false>(U, P.dst, U.partials + (P.part_begin + grp * 16 * P.n_splits) * PART_STRIDE, P.n_splits, kh,
                      rg, bq);
 }
 

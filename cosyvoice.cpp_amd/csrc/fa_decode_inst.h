@@ -9,8 +9,10 @@ namespace cvattn {
 template <int KT, int VT, bool MASK, bool BATCH>
 hipError_t launch_decode(const FaArgs &a, hipStream_t st) {
     if (a.u.total_units <= 0) return hipSuccess;
+    const DecPre &d = a.pre;
     hipLaunchKernelGGL((fa_decode_kernel<KT, VT, MASK, BATCH>), dim3((unsigned)a.u.total_units),
-                       dim3(64 * DEC_NW), 0, st, a);
+                       dim3(64 * DEC_NW), 0, st, d.k, d.v, d.q, d.k_ps, d.v_ps, d.q_ps, d.kv, d.lens, d.shape,
+                       d.units, d.scale_log2, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // single calls merge split partials with a second launch; prepared batches merge in-kernel
