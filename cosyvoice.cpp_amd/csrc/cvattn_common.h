@@ -97,7 +97,27 @@ struct FaProblem {
     // the tokens over the planned splits in runs of a multiple of split_unit tokens.
     const int32_t *n_kv_dev;
     int32_t split_unit;
+    // Mask tile classes (row-tiled kernel, masks shared by every head and sequence): byte
+    // [rg * mcls_ld + kt] tells whether the mask over row group rg's query rows and keys
+    // 64*kt .. 64*kt+63 is all zero (MCLS_ZERO), all -inf (MCLS_OFF), zero up to a per-row key
+    // and -inf after it (MCLS_PREFIX) or none of these (MCLS_MIXED);
+    // nullptr when the launch does not classify.  mcls_begin: the problem's first block in the
+    // classifying launch.
+    uint8_t *mcls;
+    int32_t mcls_ld;
+    int64_t mcls_begin;
 };
+// The classes of a launch's blocks are followed by 64 bytes per block: for an MCLS_PREFIX block,
+// the visible-prefix length of each of its query rows (row q0+i of the block at byte i), where
+// q0 is the block's first query row.  mcls_blocks: the blocks of the whole launch.
+__host__ __device__ inline uint8_t *mcls_bounds(const FaProblem &p, int64_t mcls_blocks, int64_t block) {
+    return p.mcls - p.mcls_begin + mcls_blocks + (p.mcls_begin + block) * 64;
+}
+// MCLS_PREFIX: every query row of the block is 0 up to some key and -inf from there on (the
+// edges of causal and chunk masks); the kernel then masks with the row's prefix length.
+constexpr int MCLS_ZERO = 0, MCLS_OFF = 1, MCLS_MIXED = 2, MCLS_PREFIX = 3;
+constexpr int ROWS_TILE = 64;       // keys per tile of the row-tiled kernel (the class granularity)
+constexpr int MCLS_MAX_TILES = 64; // key tiles a classified row group may have (n_kv <= 4096)
 
 // Parameters shared by every problem of one launch.
 struct FaUniform {
@@ -114,6 +134,7 @@ struct FaUniform {
     int64_t units_per_problem; // > 0 when every problem has this many workgroup units
     int64_t total_units;
     int64_t total_rows;  // sum over problems of B*H*n_q (combine grid)
+    int64_t mcls_blocks; // mask tile classes to compute before the attention launch (0: none)
     float *partials;     // workspace: split partial (m, l, O[64]) per row slot
     uint32_t *counters;  // prepared batches: split-arrival counter per (problem, b, kh, row group),
                          // CNT_STRIDE words apart, zero between launches (the merging workgroup

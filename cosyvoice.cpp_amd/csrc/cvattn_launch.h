@@ -23,10 +23,14 @@ struct FaKernelShape {
 FaKernelShape fa_shape(int n_rows, bool decode_ok);
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st);
+// A row-tiled instance for classified mask tiles exists for this K/V type pair.
+bool rows_cls_ok(int ktype, int vtype);
 // Row-tiled attention over a transposed V (vtype T_VT_F32 / T_VT_F16), single calls.
 hipError_t fa_launch_vt(int ktype, int vtype, bool mask, const FaArgs &a, hipStream_t st);
 
 hipError_t dequant_launch(int type, const void *src, float *dst, int64_t n, hipStream_t st);
+// Mask tile classes of the launch described by `a` (a.u.mcls_blocks blocks; problems' mcls set).
+hipError_t mask_classify_launch(const FaArgs &a, bool batch, hipStream_t st);
 
 // fp32 -> fp16 copy (round to nearest even, the conversion the attention kernels apply when
 // they stage fp32 K/V) of a strided 4-d view [ne0, ne1, ne2, ne3] into dense rows of dst_row

@@ -9,6 +9,9 @@ static FaLaunchFn fa_pick_decode(int mask, int batch, int ki, int vi) {
 FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_kh2(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_vt(int mask, int ki, int vti);
+FaLaunchFn fa_pick_rows_cls(int batch, int ktype, int vtype);
+
+bool rows_cls_ok(int ktype, int vtype) { return fa_pick_rows_cls(0, ktype, vtype) != nullptr; }
 
 static int type_index(int t) {
     switch (t) {
@@ -41,6 +44,10 @@ FaKernelShape fa_shape(int n_rows, bool decode_ok) {
 
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st) {
+    if (mask && !s.wsplit && s.kh == 1 && a.u.mcls_blocks > 0) {
+        const FaLaunchFn fn = fa_pick_rows_cls(batch, ktype, vtype);
+        return fn ? fn(a, st) : hipErrorInvalidValue;
+    }
     const int ki = type_index(ktype), vi = type_index(vtype);
     if (ki < 0 || vi < 0) return hipErrorInvalidValue;
     const FaLaunchFn fn = s.wsplit    ? fa_pick_decode(mask, batch, ki, vi)

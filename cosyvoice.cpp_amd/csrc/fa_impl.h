@@ -47,6 +47,7 @@ constexpr int ROWS_SETS = 1;        // 16-row sets per wave (a set shares every 
                                     // one set: 64-row workgroups, 3 resident per CU (138 VGPRs), measured
                                     // faster than two sets (128-row workgroups, 2 per CU) for prefill and DiT
 constexpr int ROWS_TS = 64;         // tokens per staged tile
+static_assert(ROWS_TS == ROWS_TILE, "mask tile classes are per staged tile");
 // halfs per LDS row of the token-major K and V tiles (64 dims + pad), and of the dim-major
 // transposed-V tile.  The pad sets which LDS banks the operand reads of a wave hit together;
 // measured on the DiT call (K / V row halfs): 72/72 43.8-44.7 us, 80/80 42.8-43.0, 80/88
@@ -207,12 +208,15 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 // take the first and second 64 tokens of each 128-token staged step, then merge through LDS.  For
 // launches with fewer row groups than CUs (prefill), where one wave per SIMD walks the whole key
 // range, this halves the chain each wave runs.
-template <int KT, int VT, bool MASK, bool BATCH, int KH>
+template <int KT, int VT, int MASK, bool BATCH, int KH>
 __global__ __launch_bounds__(64 * ROWS_NW * KH)
 // f16 K/V without mask: 3 waves per SIMD (168 VGPRs).  The masked instance does not fit 168 (it
 // spilled 104-108 bytes per lane there) and runs faster unconstrained (DiT T=1500 with a 50-frame
 // chunk mask: 73.3 -> 71.0 us).
-__attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 && !MASK ? 3 : 1)))
+// MASK: 0 none, 1 mask words read for every tile, 2 classified tiles (MCLS_*: the workgroup
+// stages only tiles that are not all -inf for its row group, and reads mask words only for mixed
+// ones; all-zero tiles run as unmasked).
+__attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 && MASK != 1 ? 3 : 1)))
 void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int TSS = TS * KH; // tokens per staged step
@@ -246,7 +250,43 @@ void fa_rows_kernel(FaArgs args) {
 
     const int t_begin = split * P.split_len;
     const int t_end = min(P.n_kv, t_begin + P.split_len);
-    const int nsteps = (max(0, t_end - t_begin) + TSS - 1) / TSS; // staged steps, uniform
+    const int nsteps_all = (max(0, t_end - t_begin) + TSS - 1) / TSS; // steps of the token range
+
+    // Mask classes (MASK 2): this row group's key tiles (at most 64) become two scalar bit masks,
+    // and the workgroup walks only the steps from its first to its last tile that is not all
+    // -inf (the visible region of a causal, chunk or window mask is one such run; an all -inf
+    // tile inside it is skipped by the waves).
+    const bool use_cls = MASK == 2 && P.mcls != nullptr; // uniform
+    uint64_t cls_zero = 0, cls_off = 0, cls_pre = 0;     // bit k: tile kt0+k all 0 / all -inf / prefix
+    int t_first = t_begin;                               // first token of staged step 0, uniform
+    int nsteps = nsteps_all, nfull = max(0, t_end - t_begin) / TSS; // staged steps / full ones, uniform
+    if constexpr (MASK == 2) {
+        static_assert(KH == 1, "mask classes are per 64-token step");
+        if (use_cls) {
+            const int kt0 = t_begin / TSS;
+            const int c = lane < nsteps_all ? P.mcls[(int64_t)rg * P.mcls_ld + kt0 + lane] : MCLS_MIXED;
+            cls_zero = __builtin_amdgcn_ballot_w64(c == MCLS_ZERO);
+            cls_off = __builtin_amdgcn_ballot_w64(c == MCLS_OFF);
+            cls_pre = __builtin_amdgcn_ballot_w64(c == MCLS_PREFIX);
+            const uint64_t live = ~cls_off & (nsteps_all >= 64 ? ~0ull : ((1ull << nsteps_all) - 1));
+            if (live == 0) {
+                nsteps = nfull = 0;
+            } else {
+                const int first = (int)__builtin_ctzll(live), last = 63 - (int)__builtin_clzll(live);
+                // the range's partial tile can only be the last step of the token range
+                const bool part = nfull < nsteps_all && last == nsteps_all - 1;
+                t_first = t_begin + first * TSS;
+                nsteps = last - first + 1;
+                nfull = nsteps - (part ? 1 : 0);
+            }
+        }
+    }
+    // the step counts are uniform: keep the loop control in scalar registers
+    nsteps = __builtin_amdgcn_readfirstlane(nsteps);
+    nfull = __builtin_amdgcn_readfirstlane(nfull);
+    t_first = __builtin_amdgcn_readfirstlane(t_first);
+    // first token of staged step i
+    auto tok = [&](int i) -> int { return t_first + i * TSS; };
 
     // ---- staging role: waves 0..2KH-1 stage K blocks, the others V blocks; thread = (token, block) ----
     // Transposed V (non-flash-attention layout): thread = (dim, 16-byte run of tokens), VNCH runs
@@ -302,8 +342,8 @@ void fa_rows_kernel(FaArgs args) {
             blk_load<VT>(rsrc, voff, t0 * nb1, r);
         }
     };
-    if (nsteps > 0) load_tile(t_begin, R0);
-    if (nsteps > 1) load_tile(t_begin + TSS, R1);
+    if (nsteps > 0) load_tile(tok(0), R0);
+    if (nsteps > 1) load_tile(tok(1), R1);
 
     // ---- this lane's query rows (one per 16-row set) and their Q operands ----
     int row[NR], iq[NR], hq[NR];
@@ -448,14 +488,29 @@ void fa_rows_kernel(FaArgs args) {
     // mask words of this wave's next full tile, loaded one step ahead (mpre_t0: their first token)
     u2 mpre[NR][NTILE];
     int mpre_t0 = -1;
-    auto qk_soft = [&](int kb, int vb, int t0, auto full_c) -> bool {
+    auto qk_soft = [&](int kb, int vb, int t0, int tn, auto full_c) -> bool {
         const _Float16 *cK = sK[kb] + hk * TS * RSK;
         auto cS = [&](int x, int b) { return x < 2 ? &sSK[kb][x][b][hk * TS] : &sSV[vb][x - 2][b][hk * TS]; };
         constexpr bool full = decltype(full_c)::value;
         // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
         // causal prefill) contributes nothing; the wave skips it
         u2 mwv[NR][NTILE];
-        if constexpr (MASK) {
+        bool mixed = MASK != 0;  // the tile adds mask words (uniform)
+        bool prefix = false;     // MASK 2: the tile keeps the first bnd[r] keys of each row (uniform)
+        int bnd[NR];
+        if constexpr (MASK == 2) {
+            // an all -inf tile is skipped, an all-zero one runs as unmasked, a prefix-shaped one
+            // reads each row's prefix length, and a mixed one reads its mask words after the QK
+            // products (so they do not add to the K operands' live registers); mixed and prefix
+            // tiles are the edges of the visible region.  (A mixed tile that is -inf for every row
+            // of the wave yields zero weights.)
+            const int k = (t0 - t_begin) / TS; // tile of the token range (uniform)
+            if constexpr (full) {
+                if ((cls_off >> k) & 1) return false;
+            }
+            prefix = use_cls && ((cls_pre >> k) & 1);
+            mixed = !((cls_zero >> k) & 1) && !prefix;
+        } else if constexpr (MASK == 1) {
             if constexpr (full) {
                 bool live = false;
                 if (mpre_t0 == t0) { // uniform
@@ -469,8 +524,8 @@ void fa_rows_kernel(FaArgs args) {
 #pragma unroll
                         for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
                 }
-                const int tn = t0 + TSS; // this wave's tile of the next step
-                if (tn + TS <= t_end) {  // uniform
+                // the words of this wave's tile of the next staged step (uniform)
+                if (tn >= 0 && tn + TS <= t_end) {
 #pragma unroll
                     for (int r = 0; r < NR; r++)
 #pragma unroll
@@ -540,10 +595,30 @@ void fa_rows_kernel(FaArgs args) {
         };
         if (need_lo) qk(std::true_type{});
         else qk(std::false_type{});
+        if constexpr (MASK == 2) {
+            if (prefix) { // uniform
+                __builtin_amdgcn_sched_barrier(0);
+                const int q0 = rg * ROWS_ROWS / U.G;
+                gu8 *b = gptr(mcls_bounds(P, U.mcls_blocks, (int64_t)rg * P.mcls_ld + t0 / TS));
+#pragma unroll
+                for (int r = 0; r < NR; r++) bnd[r] = row_ok[r] ? b[iq[r] - q0] : 0;
+            }
+            if constexpr (full) {
+                if (mixed) { // uniform
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+#pragma unroll
+                        for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
+                }
+            }
+        }
         // scores so far are base-2 logits divided by sm2 (quantized K has smul folded into its
         // scales); the mask path turns them into base-2 logits here, the others in the exponent
-        float sm2 = is_quant(KT) || MASK ? 1.0f : smul;
+        float sm2 = is_quant(KT) || MASK == 1 ? 1.0f : smul;
         const float mmul = is_quant(KT) ? 1.0f : smul;
+        // MASK 2 keeps the scores in the unmasked scale and adds mask * log2(e) / sm2
+        const float madd = 1.4426950408889634f / mmul;
 #pragma unroll
         for (int r = 0; r < NR; r++) {
             // ---- mask, bounds, softmax with a lazily raised reference maximum ----
@@ -551,7 +626,30 @@ void fa_rows_kernel(FaArgs args) {
 #pragma unroll
             for (int tt = 0; tt < NTILE; tt++) {
                 const int tb = t0 + 16 * tt + 4 * g;
-                if constexpr (MASK) {
+                if constexpr (MASK == 2) {
+                    if (prefix) { // uniform; the range's end bounds a partial tile
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int kk = 16 * tt + 4 * g + j;
+                            if (kk >= bnd[r] || (!full && t0 + kk >= t_end)) s[r][tt][j] = -INFINITY;
+                        }
+                    } else if constexpr (full) {
+                        if (mixed) { // uniform
+                            const h2 a = as_h2(mwv[r][tt][0]), c2 = as_h2(mwv[r][tt][1]);
+                            s[r][tt][0] = __builtin_fmaf((float)a[0], madd, s[r][tt][0]);
+                            s[r][tt][1] = __builtin_fmaf((float)a[1], madd, s[r][tt][1]);
+                            s[r][tt][2] = __builtin_fmaf((float)c2[0], madd, s[r][tt][2]);
+                            s[r][tt][3] = __builtin_fmaf((float)c2[1], madd, s[r][tt][3]);
+                        }
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) {
+                            const int t = tb + j;
+                            const float mv = ldg_half(mrow[r] + (int64_t)min(t, P.n_kv - 1) * 2);
+                            s[r][tt][j] = t < t_end ? __builtin_fmaf(mv, madd, s[r][tt][j]) : -INFINITY;
+                        }
+                    }
+                } else if constexpr (MASK == 1) {
                     if constexpr (full) {
                         const u2 mw = mwv[r][tt];
                         const h2 a = as_h2(mw[0]), c2 = as_h2(mw[1]);
@@ -678,51 +776,51 @@ void fa_rows_kernel(FaArgs args) {
     //      s+1 is unpacked into K buffer (s+1)&1 and V buffer (s+1)%3 from registers loaded two
     //      steps earlier; no buffer is written in the step that reads it ----
     if (nsteps > 0) {
-        write_tile(R0, 0, t_begin);
-        if (nsteps > 2) load_tile(t_begin + 2 * TSS, R0);
+        write_tile(R0, 0, tok(0));
+        if (nsteps > 2) load_tile(tok(2), R0);
     }
     __syncthreads();
     // full steps run in the loop; only the last step can be partial, and it runs after the loop
     // from the buffers the loop staged it into
-    const int nfull = max(0, t_end - t_begin) / TSS; // uniform
     const int t_half = hk * TS;                      // this wave's tokens within a step
     bool pend = false; // SHIFT: pb holds a tile whose PV product has not run (uniform per wave)
     auto step_full = [&](int s_) {
+        const int t0 = tok(s_) + t_half, tn = s_ + 1 < nsteps ? tok(s_ + 1) + t_half : -1;
         if constexpr (SHIFT) {
             if (pend) pv((s_ + NVB - 1) % NVB); // tile s_-1
-            pend = qk_soft(s_ & 1, s_ % NVB, t_begin + s_ * TSS + t_half, std::true_type{});
+            pend = qk_soft(s_ & 1, s_ % NVB, t0, tn, std::true_type{});
         } else {
-            if (qk_soft(s_ & 1, s_ % NVB, t_begin + s_ * TSS + t_half, std::true_type{})) pv(s_ % NVB);
+            if (qk_soft(s_ & 1, s_ % NVB, t0, tn, std::true_type{})) pv(s_ % NVB);
         }
     };
     for (int s0 = 0; s0 < nfull; s0 += 2) {
         // even step: stage step s0+1 from R1
         step_full(s0);
         if (s0 + 1 < nsteps) {
-            write_tile(R1, s0 + 1, t_begin + (s0 + 1) * TSS);
-            if (s0 + 3 < nsteps) load_tile(t_begin + (s0 + 3) * TSS, R1);
+            write_tile(R1, s0 + 1, tok(s0 + 1));
+            if (s0 + 3 < nsteps) load_tile(tok(s0 + 3), R1);
         }
         __syncthreads();
         if (s0 + 1 >= nfull) break;
         // odd step: stage step s0+2 from R0
         step_full(s0 + 1);
         if (s0 + 2 < nsteps) {
-            write_tile(R0, s0 + 2, t_begin + (s0 + 2) * TSS);
-            if (s0 + 4 < nsteps) load_tile(t_begin + (s0 + 4) * TSS, R0);
+            write_tile(R0, s0 + 2, tok(s0 + 2));
+            if (s0 + 4 < nsteps) load_tile(tok(s0 + 4), R0);
         }
         __syncthreads();
     }
     if (nfull < nsteps) {
         // the partial last step: with two key halves, a half's 64 tokens may be full, partial or
         // past the end (uniform per wave)
-        const int t0w = t_begin + nfull * TSS + t_half;
+        const int t0w = tok(nfull) + t_half;
         if (pend) pv((nfull + NVB - 1) % NVB);
         const int kb = nfull & 1, vb = nfull % NVB;
         if constexpr (KH == 1) {
-            pend = qk_soft(kb, vb, t0w, std::false_type{});
+            pend = qk_soft(kb, vb, t0w, -1, std::false_type{});
         } else {
-            if (t0w + TS <= t_end) pend = qk_soft(kb, vb, t0w, std::true_type{});
-            else if (t0w < t_end) pend = qk_soft(kb, vb, t0w, std::false_type{});
+            if (t0w + TS <= t_end) pend = qk_soft(kb, vb, t0w, -1, std::true_type{});
+            else if (t0w < t_end) pend = qk_soft(kb, vb, t0w, -1, std::false_type{});
             else pend = false;
         }
         if constexpr (!SHIFT) {
@@ -884,7 +982,7 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
 
 using FaLaunchFn = hipError_t (*)(const FaArgs &, hipStream_t);
 
-template <int KT, int VT, bool MASK, bool BATCH, int KH = 1>
+template <int KT, int VT, int MASK, bool BATCH, int KH = 1>
 hipError_t launch_rows(const FaArgs &a, hipStream_t st) {
     if (a.u.total_units <= 0) return hipSuccess;
     hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH, KH>), dim3((unsigned)a.u.total_units),

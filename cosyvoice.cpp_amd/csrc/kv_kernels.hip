@@ -361,6 +361,90 @@ __global__ __launch_bounds__(256) void v_idxs_kernel(int32_t *idx, const int32_t
 // n_kv[i] += delta for i < n: the device-side length update of plans prepared with a device n_kv
 // (the counterpart of shift_kv_node_pos, src/cosyvoice-kv-cache.cpp:398-408, inside a captured
 // graph).
+// Mask tile classes: one wave per (problem, row group, key tile); lane i reads query row q0+i of
+// the block (row r of the kernel is query r / G, so a 64-row group spans at most 64 query rows).
+// The block is all zero (+0 or -0), all -inf, prefix-shaped (each row 0 up to some key, -inf
+// from there on; the lane writes its row's prefix length) or none of these, over the keys below
+// n_kv (a tile the sequence ends inside is classified over its valid keys).  Only masks shared
+// by every head and sequence are classified (plane 0).
+template <bool BATCH>
+__global__ __launch_bounds__(256) void mask_classify_kernel(FaArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (blk >= a.u.mcls_blocks) return; // uniform per wave
+    const FaProblem *P = &a.p0;
+    if (BATCH && a.u.n_problems > 1) {
+        // the last problem whose first block is <= blk
+        int lo = 0, hi = a.u.n_problems - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (a.table[mid].mcls_begin <= blk) lo = mid;
+            else hi = mid - 1;
+        }
+        P = &a.table[lo];
+    }
+    const int nkt = P->mcls_ld;
+    const int64_t local = blk - P->mcls_begin;
+    const int rg = (int)(local / nkt), kt = (int)(local - (int64_t)rg * nkt);
+    int n_kv = P->n_kv;
+    if (P->n_kv_dev) n_kv = min(max(*P->n_kv_dev, 0), n_kv);
+    const int r0 = rg * 64, r1 = min(a.u.n_rows, r0 + 64) - 1;
+    const int q0 = r0 / a.u.G, q1 = r1 / a.u.G;
+    const int k0 = kt * 64;
+    const int nv = min(64, n_kv - k0); // valid keys of the tile
+    const int q = q0 + lane;
+    const bool row = q <= q1 && nv > 0;
+    bool any_nonzero = false, any_finite = false, bad = false; // bad: not prefix-shaped
+    int first_inf = max(nv, 0), last_zero = -1;
+    if (row) {
+        gu8 *m = gptr(P->mask) + (int64_t)q * P->m_nb1 + (int64_t)k0 * 2;
+        for (int c = 0; c < 8; c++) { // 8 keys a piece
+            uint32_t h[8];
+            if (8 * c + 8 <= nv) {
+                const u4 w = ldg_u128(m + 16 * c);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    h[2 * i] = w[i] & 0xffffu;
+                    h[2 * i + 1] = w[i] >> 16;
+                }
+            } else {
+                // keys past n_kv are neither read nor counted
+#pragma unroll
+                for (int i = 0; i < 8; i++) h[i] = 8 * c + i < nv ? (uint32_t)ldg_u16(m + 2 * (8 * c + i)) : 0xfc00u;
+            }
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const int kk = 8 * c + i;
+                if (kk >= nv) continue;
+                const bool inf = h[i] == 0xfc00u, zero = (h[i] & 0x7fffu) == 0u;
+                any_nonzero |= !zero;
+                any_finite |= !inf;
+                bad |= !inf && !zero;
+                if (inf) first_inf = min(first_inf, kk);
+                if (zero) last_zero = kk;
+            }
+        }
+        bad |= last_zero > first_inf;
+    }
+    int cls = MCLS_MIXED;
+    if (nv > 0) {
+        const bool nz = __builtin_amdgcn_ballot_w64(any_nonzero) != 0;
+        const bool fin = __builtin_amdgcn_ballot_w64(any_finite) != 0;
+        const bool nonprefix = __builtin_amdgcn_ballot_w64(row && bad) != 0;
+        cls = !nz ? MCLS_ZERO : !fin ? MCLS_OFF : !nonprefix ? MCLS_PREFIX : MCLS_MIXED;
+        if (cls == MCLS_PREFIX && row) mcls_bounds(*P, a.u.mcls_blocks, local)[lane] = (uint8_t)first_inf;
+    }
+    if (lane == 0) P->mcls[(int64_t)rg * nkt + kt] = (uint8_t)cls;
+}
+
+hipError_t mask_classify_launch(const FaArgs &a, bool batch, hipStream_t st) {
+    if (a.u.mcls_blocks <= 0) return hipSuccess;
+    const unsigned grid = (unsigned)((a.u.mcls_blocks + 3) / 4);
+    if (batch) hipLaunchKernelGGL(mask_classify_kernel<true>, dim3(grid), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL(mask_classify_kernel<false>, dim3(grid), dim3(256), 0, st, a);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void shift_n_kv_kernel(int32_t *n_kv, int32_t n, int32_t delta) {
     const int32_t i = (int32_t)(blockIdx.x * blockDim.x + threadIdx.x);
     if (i < n) n_kv[i] += delta;
