@@ -260,10 +260,10 @@ void fa_rows_kernel(FaArgs args) {
     uint64_t cls_zero = 0, cls_off = 0, cls_pre = 0;     // bit k: tile kt0+k all 0 / all -inf / prefix
     int t_first = t_begin;                               // first token of staged step 0, uniform
     int nsteps = nsteps_all, nfull = max(0, t_end - t_begin) / TSS; // staged steps / full ones, uniform
+    const int kt0 = t_begin / TSS;                       // class column of the range's first tile
     if constexpr (MASK == 2) {
         static_assert(KH == 1, "mask classes are per 64-token step");
         if (use_cls) {
-            const int kt0 = t_begin / TSS;
             const int c = lane < nsteps_all ? P.mcls[(int64_t)rg * P.mcls_ld + kt0 + lane] : MCLS_MIXED;
             cls_zero = __builtin_amdgcn_ballot_w64(c == MCLS_ZERO);
             cls_off = __builtin_amdgcn_ballot_w64(c == MCLS_OFF);
@@ -303,12 +303,18 @@ void fa_rows_kernel(FaArgs args) {
     const int vt_tc = st_idx % VCPD, vt_d0 = st_idx / VCPD;
     gu8 *kbase = gptr(P.k) + (int64_t)kh * P.k_nb2 + (int64_t)(bq / P.rk3) * P.k_nb3;
     gu8 *vbase = gptr(P.v) + (int64_t)kh * P.v_nb2 + (int64_t)(bq / P.rv3) * P.v_nb3;
-    const int64_t kext = P.n_kv > 0 ? (int64_t)(P.n_kv - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
+    // The tile loads are issued unconditionally, two steps ahead, also past the last step (so
+    // the compiler can count them exactly and each wait covers only the tile it needs): the K and
+    // V ranges end at the walk's last token, so loads past it read zeros without touching memory.
+    const int t_lim = min(t_end, tok(nsteps));
+    const int64_t kext = t_lim > 0 ? (int64_t)(t_lim - 1) * P.k_nb1 + 2 * dblk_bytes<KT>() : 0;
     // transposed f16: +2 bytes so the dword holding the last element is inside the range
-    // (buffer loads check whole dwords; the extra element is zeroed with the tile's tail)
+    // (buffer loads check whole dwords; the extra element is zeroed with the tile's tail).  A
+    // dim's tokens past n_kv are the next dim's; loads past the walk read them and go unused.
     const int64_t vext = P.n_kv <= 0 ? 0
                          : VTR    ? (int64_t)(HEAD - 1) * P.v_nb1 + (int64_t)P.n_kv * VES + (VES == 2 ? 2 : 0)
-                                  : (int64_t)(P.n_kv - 1) * P.v_nb1 + 2 * dblk_bytes<VT>();
+                         : t_lim > 0 ? (int64_t)(t_lim - 1) * P.v_nb1 + 2 * dblk_bytes<VT>()
+                                     : 0;
     const __amdgpu_buffer_rsrc_t rsrc = stage_k ? make_rsrc(kbase, kext) : make_rsrc(vbase, vext);
     const int nb1 = stage_k ? (int)P.k_nb1 : VTR ? VES : (int)P.v_nb1; // bytes per token
     const int voff = stage_k ? st_tok * nb1 + st_b * dblk_bytes<KT>()
@@ -342,8 +348,8 @@ void fa_rows_kernel(FaArgs args) {
             blk_load<VT>(rsrc, voff, t0 * nb1, r);
         }
     };
-    if (nsteps > 0) load_tile(tok(0), R0);
-    if (nsteps > 1) load_tile(tok(1), R1);
+    load_tile(tok(0), R0);
+    load_tile(tok(1), R1);
 
     // ---- this lane's query rows (one per 16-row set) and their Q operands ----
     int row[NR], iq[NR], hq[NR];
@@ -357,6 +363,10 @@ void fa_rows_kernel(FaArgs args) {
     }
     h8 qhi[NR][2], qlo[NR][2];
     float qsum[NR][2];
+    constexpr int BND_HELD = 4; // MASK 2: prefix tiles whose per-row lengths stay in registers
+    uint32_t bnd_pk[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) bnd_pk[r] = 0;
     float smul; // multiplies the staged K scales / raw scores into base-2 logits
     bool need_lo;
     {
@@ -376,6 +386,22 @@ void fa_rows_kernel(FaArgs args) {
                     for (int j = 0; j < 8; j++) x[r][b][j] = as_f32(ldg_u32(qp + 4 * (32 * b + 8 * g + j)));
             }
         }
+        // MASK 2: the prefix lengths of the range's first BND_HELD prefix tiles, a byte each, read
+        // beside Q (the loop then reads no memory for them)
+        if constexpr (MASK == 2) {
+            uint64_t pre = cls_pre; // uniform
+            const int q0 = rg * ROWS_ROWS / U.G;
+#pragma unroll
+            for (int i = 0; i < BND_HELD; i++) {
+                if (pre == 0) break; // uniform
+                const int k = (int)__builtin_ctzll(pre);
+                pre &= pre - 1;
+                gu8 *b = gptr(mcls_bounds(P, U.mcls_blocks, (int64_t)rg * P.mcls_ld + kt0 + k));
+#pragma unroll
+                for (int r = 0; r < NR; r++)
+                    if (row_ok[r]) bnd_pk[r] |= (uint32_t)b[iq[r] - q0] << (8 * i);
+            }
+        }
         // Q*scale exact in fp16 (up to fp16 subnormal rounding, below 2^-24) for every row?
         bool inexact = false;
 #pragma unroll
@@ -387,6 +413,12 @@ void fa_rows_kernel(FaArgs args) {
                     const float xs = row_ok[r] ? x[r][b][j] * U.scale : 0.0f;
                     inexact |= fabsf((float)(_Float16)xs - xs) > 0x1p-25f;
                 }
+        if constexpr (MASK == 2) {
+            // wait for the lengths here, with Q, not at their first use inside the loop (where the
+            // wait would also cover the tile loads issued since)
+#pragma unroll
+            for (int r = 0; r < NR; r++) asm volatile("" ::"v"(bnd_pk[r]));
+        }
         need_lo = __syncthreads_or(inexact) != 0;
         const float qmul = need_lo ? U.scale_log2 : U.scale;
         smul = need_lo ? 1.0f : 1.4426950408889634f;
@@ -492,23 +524,31 @@ void fa_rows_kernel(FaArgs args) {
         const _Float16 *cK = sK[kb] + hk * TS * RSK;
         auto cS = [&](int x, int b) { return x < 2 ? &sSK[kb][x][b][hk * TS] : &sSV[vb][x - 2][b][hk * TS]; };
         constexpr bool full = decltype(full_c)::value;
+        // a skipped tile leaves no P^T operands: pb is cleared so that the operands of the
+        // previous tile (already consumed) need not stay live beside the ones being computed
+        auto skip = [&]() -> bool {
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int kb = 0; kb < NKB; kb++) pb[r][kb][0] = pb[r][kb][1] = h8{};
+            return false;
+        };
         // masks: a tile whose mask is -inf for every row of the wave (the masked-out triangle of a
         // causal prefill) contributes nothing; the wave skips it
         u2 mwv[NR][NTILE];
         bool mixed = MASK != 0;  // the tile adds mask words (uniform)
         bool prefix = false;     // MASK 2: the tile keeps the first bnd[r] keys of each row (uniform)
         int bnd[NR];
+        int k = 0; // MASK 2: the tile's class bit (uniform)
         if constexpr (MASK == 2) {
-            // an all -inf tile is skipped, an all-zero one runs as unmasked, a prefix-shaped one
-            // reads each row's prefix length, and a mixed one reads its mask words after the QK
-            // products (so they do not add to the K operands' live registers); mixed and prefix
-            // tiles are the edges of the visible region.  (A mixed tile that is -inf for every row
-            // of the wave yields zero weights.)
-            const int k = (t0 - t_begin) / TS; // tile of the token range (uniform)
-            if constexpr (full) {
-                if ((cls_off >> k) & 1) return false;
-            }
-            prefix = use_cls && ((cls_pre >> k) & 1);
+            // an all-zero tile runs as unmasked, a prefix-shaped one masks each row past its
+            // prefix length, an all -inf one inside the walked range (a hole; the range itself
+            // starts and ends at visible tiles) runs as a prefix tile of length 0, and a mixed one
+            // reads its mask words after the QK products (so they do not add to the K operands'
+            // live registers).  Skipping holes instead would keep a second set of P^T operands
+            // live across the loop.
+            k = (t0 - t_begin) / TS;
+            prefix = use_cls && (((cls_pre | cls_off) >> k) & 1);
             mixed = !((cls_zero >> k) & 1) && !prefix;
         } else if constexpr (MASK == 1) {
             if constexpr (full) {
@@ -542,7 +582,7 @@ void fa_rows_kernel(FaArgs args) {
                         live |= row_ok[r] && ((mwv[r][tt][0] & 0xffffu) != 0xfc00u || (mwv[r][tt][0] >> 16) != 0xfc00u ||
                                               (mwv[r][tt][1] & 0xffffu) != 0xfc00u || (mwv[r][tt][1] >> 16) != 0xfc00u);
                     }
-                if (__builtin_amdgcn_ballot_w64(live) == 0) return false; // uniform
+                if (__builtin_amdgcn_ballot_w64(live) == 0) return skip(); // uniform
             }
         }
         f4 s[NR][NTILE];
@@ -597,11 +637,27 @@ void fa_rows_kernel(FaArgs args) {
         else qk(std::false_type{});
         if constexpr (MASK == 2) {
             if (prefix) { // uniform
-                __builtin_amdgcn_sched_barrier(0);
-                const int q0 = rg * ROWS_ROWS / U.G;
-                gu8 *b = gptr(mcls_bounds(P, U.mcls_blocks, (int64_t)rg * P.mcls_ld + t0 / TS));
+                // the range's first BND_HELD prefix tiles have their lengths in registers; later
+                // ones (and only they) read them here
+                const int idx = __builtin_popcountll(cls_pre & ((1ull << k) - 1)); // uniform
+                if ((cls_off >> k) & 1) {
 #pragma unroll
-                for (int r = 0; r < NR; r++) bnd[r] = row_ok[r] ? b[iq[r] - q0] : 0;
+                    for (int r = 0; r < NR; r++) bnd[r] = 0;
+                } else if (idx < BND_HELD) {
+#pragma unroll
+                    for (int r = 0; r < NR; r++) bnd[r] = (bnd_pk[r] >> (8 * idx)) & 0xff;
+                } else {
+                    __builtin_amdgcn_sched_barrier(0);
+                    const int q0 = rg * ROWS_ROWS / U.G;
+                    gu8 *b = gptr(mcls_bounds(P, U.mcls_blocks, (int64_t)rg * P.mcls_ld + kt0 + k));
+#pragma unroll
+                    for (int r = 0; r < NR; r++) {
+                        bnd[r] = row_ok[r] ? b[iq[r] - q0] : 0;
+                        // complete the load inside this branch: a load still pending where the
+                        // branches meet would make the other paths wait for every load in flight
+                        asm volatile("" ::"v"(bnd[r]));
+                    }
+                }
             }
             if constexpr (full) {
                 if (mixed) { // uniform
@@ -610,6 +666,11 @@ void fa_rows_kernel(FaArgs args) {
                     for (int r = 0; r < NR; r++)
 #pragma unroll
                         for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
+                    // complete the loads inside this branch (as for the prefix lengths above)
+#pragma unroll
+                    for (int r = 0; r < NR; r++)
+#pragma unroll
+                        for (int tt = 0; tt < NTILE; tt++) asm volatile("" ::"v"(mwv[r][tt]));
                 }
             }
         }
@@ -623,16 +684,21 @@ void fa_rows_kernel(FaArgs args) {
         for (int r = 0; r < NR; r++) {
             // ---- mask, bounds, softmax with a lazily raised reference maximum ----
             float mx = -INFINITY;
+            // prefix tiles: key 16tt + 4g + j of the tile is visible below the row's prefix length
+            // (and the range's end, in a partial tile); the lane's offset 4g moves to the bound so
+            // the comparisons are against constants
+            int plim = 0;
+            if constexpr (MASK == 2) {
+                if (prefix) plim = (full ? bnd[r] : min(bnd[r], t_end - t0)) - 4 * g;
+            }
 #pragma unroll
             for (int tt = 0; tt < NTILE; tt++) {
                 const int tb = t0 + 16 * tt + 4 * g;
                 if constexpr (MASK == 2) {
-                    if (prefix) { // uniform; the range's end bounds a partial tile
+                    if (prefix) { // uniform
 #pragma unroll
-                        for (int j = 0; j < 4; j++) {
-                            const int kk = 16 * tt + 4 * g + j;
-                            if (kk >= bnd[r] || (!full && t0 + kk >= t_end)) s[r][tt][j] = -INFINITY;
-                        }
+                        for (int j = 0; j < 4; j++)
+                            if (16 * tt + j >= plim) s[r][tt][j] = -INFINITY;
                     } else if constexpr (full) {
                         if (mixed) { // uniform
                             const h2 a = as_h2(mwv[r][tt][0]), c2 = as_h2(mwv[r][tt][1]);
@@ -775,10 +841,8 @@ void fa_rows_kernel(FaArgs args) {
     //      in pb across the barrier), then QK and softmax of tile s (K buffer s&1), while tile
     //      s+1 is unpacked into K buffer (s+1)&1 and V buffer (s+1)%3 from registers loaded two
     //      steps earlier; no buffer is written in the step that reads it ----
-    if (nsteps > 0) {
-        write_tile(R0, 0, tok(0));
-        if (nsteps > 2) load_tile(tok(2), R0);
-    }
+    if (nsteps > 0) write_tile(R0, 0, tok(0));
+    load_tile(tok(2), R0);
     __syncthreads();
     // full steps run in the loop; only the last step can be partial, and it runs after the loop
     // from the buffers the loop staged it into
@@ -793,21 +857,25 @@ void fa_rows_kernel(FaArgs args) {
             if (qk_soft(s_ & 1, s_ % NVB, t0, tn, std::true_type{})) pv(s_ % NVB);
         }
     };
-    for (int s0 = 0; s0 < nfull; s0 += 2) {
+    // Every step writes the next tile and issues the loads of the one after (past the walk they
+    // stage zeros into buffers nothing reads), and the loop has no early exit: the tile loads
+    // are then counted exactly on every path, so each write waits only for its own tile.
+    int s0 = 0;
+    for (; s0 + 1 < nfull; s0 += 2) {
         // even step: stage step s0+1 from R1
         step_full(s0);
-        if (s0 + 1 < nsteps) {
-            write_tile(R1, s0 + 1, tok(s0 + 1));
-            if (s0 + 3 < nsteps) load_tile(tok(s0 + 3), R1);
-        }
+        write_tile(R1, s0 + 1, tok(s0 + 1));
+        load_tile(tok(s0 + 3), R1);
         __syncthreads();
-        if (s0 + 1 >= nfull) break;
         // odd step: stage step s0+2 from R0
         step_full(s0 + 1);
-        if (s0 + 2 < nsteps) {
-            write_tile(R0, s0 + 2, tok(s0 + 2));
-            if (s0 + 4 < nsteps) load_tile(tok(s0 + 4), R0);
-        }
+        write_tile(R0, s0 + 2, tok(s0 + 2));
+        load_tile(tok(s0 + 4), R0);
+        __syncthreads();
+    }
+    if (s0 < nfull) { // an odd count of full steps: the last one
+        step_full(s0);
+        write_tile(R1, s0 + 1, tok(s0 + 1));
         __syncthreads();
     }
     if (nfull < nsteps) {
