@@ -517,9 +517,18 @@ void fa_rows_kernel(FaArgs args) {
     // tokens t0..t0+TS), leaving its P^T operands in pb; `full_c` (std::true_type) says every
     // token of the tile is in range, so no bounds code is emitted (t0: this wave's 64 tokens, key
     // half hk of the staged step).  False when the mask removes the whole tile for this wave.
-    // mask words of this wave's next full tile, loaded one step ahead (mpre_t0: their first token)
+    // MASK 1: mask words of this wave's next full tile, loaded one step ahead; here the first one's
+    // (a wave whose first tile is partial never reads them)
     u2 mpre[NR][NTILE];
-    int mpre_t0 = -1;
+    if constexpr (MASK == 1) {
+        const int t0 = tok(0) + hk * TS;
+        if (t0 + TS <= t_end) { // uniform
+#pragma unroll
+            for (int r = 0; r < NR; r++)
+#pragma unroll
+                for (int tt = 0; tt < NTILE; tt++) mpre[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
+        }
+    }
     auto qk_soft = [&](int kb, int vb, int t0, int tn, auto full_c) -> bool {
         const _Float16 *cK = sK[kb] + hk * TS * RSK;
         auto cS = [&](int x, int b) { return x < 2 ? &sSK[kb][x][b][hk * TS] : &sSV[vb][x - 2][b][hk * TS]; };
@@ -553,27 +562,19 @@ void fa_rows_kernel(FaArgs args) {
         } else if constexpr (MASK == 1) {
             if constexpr (full) {
                 bool live = false;
-                if (mpre_t0 == t0) { // uniform
+                // this tile's words were loaded one step ahead (the wave's first full tile's
+                // before the pipeline); the words of its tile of the next staged step are loaded
+                // now.  Past the last full tile the current one is read again: the loads are then
+                // unconditional, and the waits for them and for the staged tiles count exactly.
 #pragma unroll
-                    for (int r = 0; r < NR; r++)
+                for (int r = 0; r < NR; r++)
 #pragma unroll
-                        for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = mpre[r][tt];
-                } else {
+                    for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = mpre[r][tt];
+                const int tp = tn >= 0 && tn + TS <= t_end ? tn : t0;
 #pragma unroll
-                    for (int r = 0; r < NR; r++)
+                for (int r = 0; r < NR; r++)
 #pragma unroll
-                        for (int tt = 0; tt < NTILE; tt++) mwv[r][tt] = ldg_u64(mrow[r] + (int64_t)(t0 + 16 * tt + 4 * g) * 2);
-                }
-                // the words of this wave's tile of the next staged step (uniform)
-                if (tn >= 0 && tn + TS <= t_end) {
-#pragma unroll
-                    for (int r = 0; r < NR; r++)
-#pragma unroll
-                        for (int tt = 0; tt < NTILE; tt++) mpre[r][tt] = ldg_u64(mrow[r] + (int64_t)(tn + 16 * tt + 4 * g) * 2);
-                    mpre_t0 = tn;
-                } else {
-                    mpre_t0 = -1;
-                }
+                    for (int tt = 0; tt < NTILE; tt++) mpre[r][tt] = ldg_u64(mrow[r] + (int64_t)(tp + 16 * tt + 4 * g) * 2);
 #pragma unroll
                 for (int r = 0; r < NR; r++)
 #pragma unroll
