@@ -139,6 +139,49 @@ def time_graph(torch, launch_fn, n_per_graph, warmup_steps, repeats=TIMED_REPEAT
     return time_graphs(torch, [launch_fn], n_per_graph, warmup_steps, repeats)[0]
 
 
+def decode_cadence(lib, cvattn, torch, dev, problem, n_copies, keep):
+    """The real decode cadence: 24 dependent per-layer launches per token, from plans prepared on
+    the host and from plans reading a device-resident n_kv (one graph replay per token runs
+    [cvattn_shift_n_kv +1, 24 layer launches] for each copy, so n_kv grows by one per replay).
+    Returns (ms per token, ms per token with device n_kv)."""
+    layer_plans = [[make_plan(lib, cvattn, torch, dev, [problem(r, l)], keep) for l in range(L)]
+                   for r in range(n_copies)]
+
+    def launch_layers(s):
+        for r in range(n_copies):
+            for p in layer_plans[r]:
+                assert lib.fa_batch_launch(p, s) == cvattn.OK
+
+    ms_seq = time_graph(torch, launch_layers, n_copies, n_copies)
+    log(f"decode 24 sequential layer launches: {ms_seq * 1e3:.2f} us/token")
+
+    n_kv_dev = torch.full((n_copies,), NKV - 64, dtype=torch.int32, device=dev)
+    dyn_plans = []
+    for r in range(n_copies):
+        row = []
+        for l_ in range(L):
+            probs = [problem(r, l_)]
+            wsb = lib.fa_batch_workspace(probs)
+            ws_ = torch.empty(wsb, dtype=torch.uint8, device=dev)
+            keep.append(ws_)
+            rc, pl = lib.fa_batch_prepare_dynamic(probs, 1.0 / math.sqrt(D), n_kv_dev[r:].data_ptr(), 0,
+                                                  ws_.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
+            assert rc == cvattn.OK, lib.status_string(rc)
+            keep.append(pl)
+            row.append(pl)
+        dyn_plans.append(row)
+
+    def launch_dynamic(s):
+        for r in range(n_copies):
+            assert lib.shift_n_kv(n_kv_dev[r:].data_ptr(), 1, 1, s) == cvattn.OK
+            for p in dyn_plans[r]:
+                assert lib.fa_batch_launch(p, s) == cvattn.OK
+
+    ms_dyn = time_graph(torch, launch_dynamic, n_copies, 0)
+    log(f"decode per-token graph with device n_kv: {ms_dyn * 1e3:.2f} us/token")
+    return ms_seq, ms_dyn
+
+
 def bench_dit(lib, cvattn, torch, dev):
     """Flow-DiT attention layer call: T=1500, B=2, 16 heads, fp16 q/k/v views, no mask, through a
     prepared batch (10 calls per graph replay)."""
@@ -534,6 +577,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-dit", action="store_true", help="skip the DiT legs")
     ap.add_argument("--no-extra", action="store_true", help="skip the prefill, DiT-stream, serving and single-call legs")
+    ap.add_argument("--no-cadence", action="store_true",
+                    help="skip the per-layer decode cadence legs (counter passes over the 24-layer step alone)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run 256 MiB device copies (reference kernels for the HBM counters)")
     ap.add_argument("--stream-floor", action="store_true",
@@ -595,46 +640,12 @@ def main():
     gbs = bytes_step / (ms * 1e-3) / 1e9
     log(f"decode 24x4096 batched: {ms * 1e3:.2f} us/step (median of {TIMED_REPEATS} replays of {K}), {gbs:.0f} GB/s")
 
-    # real decode cadence: 24 dependent per-layer launches per token
-    layer_plans = [[make_plan(lib, cvattn, torch, dev, [problem(r, l)], keep) for l in range(L)]
-                   for r in range(n_copies)]
-
-    def launch_layers(s):
-        for r in range(n_copies):
-            for p in layer_plans[r]:
-                assert lib.fa_batch_launch(p, s) == cvattn.OK
-
-    ms_seq = time_graph(torch, launch_layers, n_copies, n_copies)
-    log(f"decode 24 sequential layer launches: {ms_seq * 1e3:.2f} us/token")
-
-    # the same cadence from plans with a device-resident n_kv: one graph replay per token runs
-    # [cvattn_shift_n_kv +1, 24 layer launches] for each copy, so n_kv grows by one per replay
-    n_kv_dev = torch.full((n_copies,), NKV - 64, dtype=torch.int32, device=dev)
-    dyn_plans = []
-    for r in range(n_copies):
-        row = []
-        for l_ in range(L):
-            probs = [problem(r, l_)]
-            wsb = lib.fa_batch_workspace(probs)
-            ws_ = torch.empty(wsb, dtype=torch.uint8, device=dev)
-            keep.append(ws_)
-            rc, pl = lib.fa_batch_prepare_dynamic(probs, 1.0 / math.sqrt(D), n_kv_dev[r:].data_ptr(), 0,
-                                                  ws_.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream)
-            assert rc == cvattn.OK, lib.status_string(rc)
-            keep.append(pl)
-            row.append(pl)
-        dyn_plans.append(row)
-
-    def launch_dynamic(s):
-        for r in range(n_copies):
-            assert lib.shift_n_kv(n_kv_dev[r:].data_ptr(), 1, 1, s) == cvattn.OK
-            for p in dyn_plans[r]:
-                assert lib.fa_batch_launch(p, s) == cvattn.OK
-
-    ms_dyn = time_graph(torch, launch_dynamic, n_copies, 0)
-    log(f"decode per-token graph with device n_kv: {ms_dyn * 1e3:.2f} us/token")
+    ms_seq = ms_dyn = None
+    if not args.no_cadence:
+        ms_seq, ms_dyn = decode_cadence(lib, cvattn, torch, dev, problem, n_copies, keep)
 
     extra = {}
+
     if not args.no_dit:
         extra["dit_attn"] = bench_dit(lib, cvattn, torch, dev)
         log(f"dit T=1500: {extra['dit_attn']['ms_per_layer_call'] * 1e3:.1f} us/call, "
@@ -690,10 +701,11 @@ def main():
             "bytes_per_step": bytes_step,
         },
         # the decode rate a token loop reaches: layer l+1 needs layer l's output, so one launch per layer
-        "tok_per_s": 1000.0 / ms_seq,
-        "us_per_token": ms_seq * 1e3,
+        "tok_per_s": 1000.0 / ms_seq if ms_seq else None,
+        "us_per_token": ms_seq * 1e3 if ms_seq else None,
         "tok_per_s_basis": "24 dependent one-layer launches per token (prepared plans, graph-replayed)",
-        "decode_graph_device_n_kv": {"us_per_token": ms_dyn * 1e3, "tok_per_s": 1000.0 / ms_dyn,
+        "decode_graph_device_n_kv": {"us_per_token": ms_dyn * 1e3 if ms_dyn else None,
+                                     "tok_per_s": 1000.0 / ms_dyn if ms_dyn else None,
                                      "workload": "per token one graph replay: cvattn_shift_n_kv + 24 layer launches "
                                                  "of plans prepared with a device n_kv (4033.. tokens, capacity 4096)"},
         "layer_batched_synthetic": {"tok_per_s": 1000.0 / ms,

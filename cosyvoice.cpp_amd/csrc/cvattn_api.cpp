@@ -392,7 +392,7 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
     if (pl->mcls_ld) {
         // the classes, then the prefix lengths (64 per block)
         pl->mcls_off = bytes = align_up(bytes, kAlign);
-        bytes += (size_t)sh.n_rowgroups * pl->mcls_ld * 65;
+        bytes += (size_t)mcls_table_bytes((int64_t)sh.n_rowgroups * pl->mcls_ld);
     }
     pl->ws_bytes = bytes;
     return CVATTN_OK;
@@ -498,6 +498,7 @@ static int run_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvat
     rc = check_dst(dst, pl.sh);
     if (rc) return rc;
     if (ws_bytes < pl.ws_bytes || (pl.ws_bytes && !ws)) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
+    if (pl.ws_bytes && ((uintptr_t)ws & (kAlign - 1))) return CVATTN_ERR_BAD_ARGS; // tables use aligned vector stores
     cvattn_tensor k16, v16;
     CvtF16Args cvt[2];
     int n_cvt = 0;
@@ -686,7 +687,7 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
             // the classes of every problem, then their prefix lengths (64 per block)
             lay->mcls_off = lay->total_bytes = align_up(lay->total_bytes, kAlign);
             lay->mcls_blocks = blocks;
-            lay->total_bytes += (size_t)blocks * 65;
+            lay->total_bytes += (size_t)mcls_table_bytes(blocks);
         } else if (table) {
             for (int i = 0; i < n; i++) (*table)[i].mcls_ld = 0;
         }
@@ -713,6 +714,7 @@ static int prepare_batch(const cvattn_fa_problem *problems, int n, float scale, 
     int rc = plan_batch(problems, n, &table, &sh, &lay, n_kv_dev, n_kv_stride);
     if (rc) return rc;
     if (!ws || ws_bytes < lay.total_bytes) return CVATTN_ERR_WORKSPACE_TOO_SMALL;
+    if ((uintptr_t)ws & (kAlign - 1)) return CVATTN_ERR_BAD_ARGS; // tables use aligned vector stores
     BatchPlan bp;
     std::memset(&bp, 0, sizeof(bp));
     bp.magic = kPlanMagic;

@@ -107,11 +107,13 @@ struct FaProblem {
     int32_t mcls_ld;
     int64_t mcls_begin;
 };
-// The classes of a launch's blocks are followed by 64 bytes per block: for an MCLS_PREFIX block,
-// the visible-prefix length of each of its query rows (row q0+i of the block at byte i), where
-// q0 is the block's first query row.  mcls_blocks: the blocks of the whole launch.
+// The classes of a launch's blocks (padded to 64 bytes) are followed by 64 bytes per block: for
+// an MCLS_PREFIX block, the visible-prefix length of each of its query rows (row q0+i of the
+// block at byte i), where q0 is the block's first query row.  mcls_blocks: the blocks of the
+// whole launch.  The whole table takes mcls_table_bytes(mcls_blocks) from a 64-aligned base.
+__host__ __device__ inline int64_t mcls_table_bytes(int64_t mcls_blocks) { return (mcls_blocks + 63) / 64 * 64 + 64 * mcls_blocks; }
 __host__ __device__ inline uint8_t *mcls_bounds(const FaProblem &p, int64_t mcls_blocks, int64_t block) {
-    return p.mcls - p.mcls_begin + mcls_blocks + (p.mcls_begin + block) * 64;
+    return p.mcls - p.mcls_begin + (mcls_blocks + 63) / 64 * 64 + (p.mcls_begin + block) * 64;
 }
 // MCLS_PREFIX: every query row of the block is 0 up to some key and -inf from there on (the
 // edges of causal and chunk masks); the kernel then masks with the row's prefix length.

@@ -367,64 +367,91 @@ __global__ __launch_bounds__(256) void v_idxs_kernel(int32_t *idx, const int32_t
 // from there on; the lane writes its row's prefix length) or none of these, over the keys below
 // n_kv (a tile the sequence ends inside is classified over its valid keys).  Only masks shared
 // by every head and sequence are classified (plane 0).
-template <bool BATCH>
-__global__ __launch_bounds__(256) void mask_classify_kernel(FaArgs a) {
-    const int lane = threadIdx.x & 63;
-    const int64_t blk = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (blk >= a.u.mcls_blocks) return; // uniform per wave
-    const FaProblem *P = &a.p0;
-    if (BATCH && a.u.n_problems > 1) {
-        // the last problem whose first block is <= blk
-        int lo = 0, hi = a.u.n_problems - 1;
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (a.table[mid].mcls_begin <= blk) lo = mid;
-            else hi = mid - 1;
-        }
-        P = &a.table[lo];
-    }
-    const int nkt = P->mcls_ld;
-    const int64_t local = blk - P->mcls_begin;
-    const int rg = (int)(local / nkt), kt = (int)(local - (int64_t)rg * nkt);
-    int n_kv = P->n_kv;
-    if (P->n_kv_dev) n_kv = min(max(*P->n_kv_dev, 0), n_kv);
-    const int r0 = rg * 64, r1 = min(a.u.n_rows, r0 + 64) - 1;
-    const int q0 = r0 / a.u.G, q1 = r1 / a.u.G;
+// One block (row group rg, key tile kt) of a problem: lane i reads query row q0+i (64 keys as
+// eight 16-byte pieces, all in flight at once).  A row of only +-0 or only -inf is told by two OR
+// reductions over its 32 words; only rows with both (the edges of the visible region) are
+// scanned key by key.  Writes the class byte and, for a prefix-shaped block, the 64 prefix
+// lengths.
+__device__ __forceinline__ void classify_block(const void *mask, int64_t m_nb1, int rg, int kt, int n_kv, int n_rows,
+                                               int G, uint8_t *cls_out, uint8_t *bnd, int lane) {
+    const int r0 = rg * 64, r1 = min(n_rows, r0 + 64) - 1;
+    const int q0 = r0 / G, q1 = r1 / G;
     const int k0 = kt * 64;
     const int nv = min(64, n_kv - k0); // valid keys of the tile
     const int q = q0 + lane;
     const bool row = q <= q1 && nv > 0;
     bool any_nonzero = false, any_finite = false, bad = false; // bad: not prefix-shaped
-    int first_inf = max(nv, 0), last_zero = -1;
+    int first_inf = max(nv, 0);
     if (row) {
-        gu8 *m = gptr(P->mask) + (int64_t)q * P->m_nb1 + (int64_t)k0 * 2;
-        for (int c = 0; c < 8; c++) { // 8 keys a piece
-            uint32_t h[8];
+        gu8 *m = gptr(mask) + (int64_t)q * m_nb1 + (int64_t)k0 * 2;
+        // whole pieces below n_kv as 16-byte loads, the piece n_kv ends inside key by key; keys
+        // past n_kv are neither read nor counted (they read as -inf here, and the scan stops at
+        // nv).  The piece conditions are uniform, and every load is issued before any use.
+        u4 w[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
             if (8 * c + 8 <= nv) {
-                const u4 w = ldg_u128(m + 16 * c);
+                w[c] = ldg_u128(m + 16 * c);
+            } else if (8 * c < nv) {
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
-                    h[2 * i] = w[i] & 0xffffu;
-                    h[2 * i + 1] = w[i] >> 16;
+                    const int kk = 8 * c + 2 * i;
+                    const uint32_t lo = kk < nv ? (uint32_t)ldg_u16(m + 2 * kk) : 0xfc00u;
+                    const uint32_t hi = kk + 1 < nv ? (uint32_t)ldg_u16(m + 2 * kk + 2) : 0xfc00u;
+                    w[c][i] = lo | (hi << 16);
                 }
             } else {
-                // keys past n_kv are neither read nor counted
-#pragma unroll
-                for (int i = 0; i < 8; i++) h[i] = 8 * c + i < nv ? (uint32_t)ldg_u16(m + 2 * (8 * c + i)) : 0xfc00u;
-            }
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const int kk = 8 * c + i;
-                if (kk >= nv) continue;
-                const bool inf = h[i] == 0xfc00u, zero = (h[i] & 0x7fffu) == 0u;
-                any_nonzero |= !zero;
-                any_finite |= !inf;
-                bad |= !inf && !zero;
-                if (inf) first_inf = min(first_inf, kk);
-                if (zero) last_zero = kk;
+                w[c] = u4{0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u, 0xfc00fc00u};
             }
         }
-        bad |= last_zero > first_inf;
+        uint32_t orz = 0, orn = 0; // OR of the magnitudes / of the differences from -inf
+#pragma unroll
+        for (int c = 0; c < 8; c++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                orz |= w[c][i] & 0x7fff7fffu;
+                orn |= w[c][i] ^ 0xfc00fc00u;
+            }
+        if (nv == 64 && orz == 0) { // every key +-0
+            any_finite = true;
+        } else if (nv == 64 && orn == 0) { // every key -inf
+            any_nonzero = true;
+            first_inf = 0;
+        } else {
+            // an edge row: its first -inf key f, then one check that keys below f are +-0 and
+            // keys from f on (below nv) are -inf; pieces and halves are compile-time indexes and
+            // the bounds are compares, not branches
+            int f = nv;
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t x = w[c][i];
+                    const int k = 8 * c + 2 * i;
+                    const int fk = (x & 0xffffu) == 0xfc00u ? k : (x >> 16) == 0xfc00u ? k + 1 : 64;
+                    f = min(f, fk);
+                }
+            bool ok = true, nz = false, fin = false;
+#pragma unroll
+            for (int c = 0; c < 8; c++)
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const uint32_t x = w[c][i];
+                    const int k = 8 * c + 2 * i;
+                    const uint32_t lo = x & 0xffffu, hi = x >> 16;
+                    const bool lz = (lo & 0x7fffu) == 0u, hz = (hi & 0x7fffu) == 0u;
+                    const bool li = lo == 0xfc00u, hi_i = hi == 0xfc00u;
+                    // keys past nv read as -inf and count as neither
+                    ok &= k >= nv || (k < f ? lz : li);
+                    ok &= k + 1 >= nv || (k + 1 < f ? hz : hi_i);
+                    nz |= (k < nv && !lz) || (k + 1 < nv && !hz);
+                    fin |= (k < nv && !li) || (k + 1 < nv && !hi_i);
+                }
+            any_nonzero = nz;
+            any_finite = fin;
+            bad = !ok;
+            first_inf = f;
+        }
     }
     int cls = MCLS_MIXED;
     if (nv > 0) {
@@ -432,16 +459,69 @@ __global__ __launch_bounds__(256) void mask_classify_kernel(FaArgs a) {
         const bool fin = __builtin_amdgcn_ballot_w64(any_finite) != 0;
         const bool nonprefix = __builtin_amdgcn_ballot_w64(row && bad) != 0;
         cls = !nz ? MCLS_ZERO : !fin ? MCLS_OFF : !nonprefix ? MCLS_PREFIX : MCLS_MIXED;
-        if (cls == MCLS_PREFIX && row) mcls_bounds(*P, a.u.mcls_blocks, local)[lane] = (uint8_t)first_inf;
+        if (cls == MCLS_PREFIX) {
+            // four lanes' lengths a dword (the table is 64-byte aligned): one 64-byte store, not
+            // 64 byte stores
+            const uint32_t b = (uint32_t)first_inf & 0xffu;
+            const uint32_t b1 = __shfl_down(b, 1), b2 = __shfl_down(b, 2), b3 = __shfl_down(b, 3);
+            if ((lane & 3) == 0) ((uint32_t *)bnd)[lane >> 2] = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
+        }
     }
-    if (lane == 0) P->mcls[(int64_t)rg * nkt + kt] = (uint8_t)cls;
+    if (lane == 0) *cls_out = (uint8_t)cls;
+}
+
+template <bool BATCH>
+__global__ __launch_bounds__(256) void mask_classify_kernel(FaArgs a) {
+    const int lane = threadIdx.x & 63;
+    // the wave's block (uniform: the problem lookup and its fields stay on the scalar unit)
+    const int64_t blk = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blk >= a.u.mcls_blocks) return;
+    FaProblem P;
+    if (!BATCH || a.u.n_problems == 1) {
+        P = a.p0;
+    } else {
+        // the last problem whose first block is <= blk
+        int lo = 0, hi = a.u.n_problems - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (a.table[mid].mcls_begin <= blk) lo = mid;
+            else hi = mid - 1;
+        }
+        P = a.table[__builtin_amdgcn_readfirstlane(lo)];
+    }
+    const int nkt = P.mcls_ld;
+    const int64_t local = blk - P.mcls_begin;
+    const int rg = (int)(local / nkt), kt = (int)(local - (int64_t)rg * nkt);
+    int n_kv = P.n_kv;
+    if (P.n_kv_dev) n_kv = min(max(*P.n_kv_dev, 0), n_kv);
+    classify_block(P.mask, P.m_nb1, rg, kt, n_kv, a.u.n_rows, a.u.G, P.mcls + local, mcls_bounds(P, a.u.mcls_blocks, local), lane);
+}
+
+// The one-problem launch with a host-set n_kv (every DiT call): its few arguments are scalars in
+// the first kernel-argument dwords, which the compiled kernel receives in SGPRs (kernarg
+// preloading takes scalar arguments, not aggregates), so a wave reads no argument memory before
+// its mask loads: the kernel is two memory round trips (mask, class stores) instead of four.
+__global__ __launch_bounds__(256) void mask_classify_one(const void *mask, uint8_t *mcls, int32_t m_nb1, int32_t nkt,
+                                                         int32_t blocks, int32_t n_kv, int32_t n_rows, int32_t G) {
+    const int lane = threadIdx.x & 63;
+    const int blk = (int)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (blk >= blocks) return;
+    const int rg = blk / nkt, kt = blk - rg * nkt;
+    classify_block(mask, m_nb1, rg, kt, n_kv, n_rows, G, mcls + blk, mcls + (blocks + 63) / 64 * 64 + (int64_t)blk * 64, lane);
 }
 
 hipError_t mask_classify_launch(const FaArgs &a, bool batch, hipStream_t st) {
     if (a.u.mcls_blocks <= 0) return hipSuccess;
     const unsigned grid = (unsigned)((a.u.mcls_blocks + 3) / 4);
-    if (batch) hipLaunchKernelGGL(mask_classify_kernel<true>, dim3(grid), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL(mask_classify_kernel<false>, dim3(grid), dim3(256), 0, st, a);
+    const FaProblem &p = a.p0;
+    if ((!batch || a.u.n_problems == 1) && !p.n_kv_dev && p.m_nb1 <= INT32_MAX && a.u.mcls_blocks <= INT32_MAX / 64) {
+        hipLaunchKernelGGL(mask_classify_one, dim3(grid), dim3(256), 0, st, (const void *)p.mask, p.mcls, (int32_t)p.m_nb1,
+                           p.mcls_ld, (int32_t)a.u.mcls_blocks, p.n_kv, a.u.n_rows, a.u.G);
+    } else if (batch) {
+        hipLaunchKernelGGL(mask_classify_kernel<true>, dim3(grid), dim3(256), 0, st, a);
+    } else {
+        hipLaunchKernelGGL(mask_classify_kernel<false>, dim3(grid), dim3(256), 0, st, a);
+    }
     return hipGetLastError();
 }
 

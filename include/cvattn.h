@@ -96,7 +96,8 @@ CVATTN_API size_t cvattn_flash_attn_ext_workspace(const cvattn_tensor *q, const 
 /* Replaces the GGML_OP_FLASH_ATTN_EXT node built by ggml_flash_attn_ext(ctx, q, k, v, mask,
  * scale, max_bias, logit_softcap) + ggml_flash_attn_ext_set_prec(node, prec) at
  * src/cosyvoice-kv-cache.cpp:383-384 and src/cosyvoice-graph.cpp:375-376.  Asynchronous on
- * `stream`; `ws` must hold cvattn_flash_attn_ext_workspace() bytes (may be NULL when that is 0). */
+ * `stream`; `ws` must hold cvattn_flash_attn_ext_workspace() bytes (may be NULL when that is 0)
+ * and be 256-byte aligned (hipMalloc and torch allocations are); else CVATTN_ERR_BAD_ARGS. */
 CVATTN_API int cvattn_flash_attn_ext(const cvattn_tensor *q, const cvattn_tensor *k,
                                      const cvattn_tensor *v, const cvattn_tensor *mask,
                                      const cvattn_tensor *dst, float scale, float max_bias,
@@ -124,7 +125,8 @@ CVATTN_API int cvattn_flash_attn_ext_noalloc(const cvattn_tensor *q, const cvatt
  * (tools/server/cosyvoice-server.cpp:318-323) gives many such nodes per step.  All problems must
  * share q/k/v/mask presence and types, D/Dv, H, H_kv, n_q and B; n_kv, pointers and strides may
  * differ per problem (ragged KV lengths).
- *   cvattn_fa_batch_workspace   bytes needed for n problems (includes the device problem table)
+ *   cvattn_fa_batch_workspace   bytes needed for n problems (includes the device problem table);
+ *                               the workspace must be 256-byte aligned (else CVATTN_ERR_BAD_ARGS)
  *   cvattn_fa_batch_prepare     validates the problems, uploads the problem table and zeroed
  *                               split counters into ws (one host->device copy on `stream`, then
  *                               waits for it: a set-up call) and fills a host-side plan
