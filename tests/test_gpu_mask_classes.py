@@ -105,3 +105,26 @@ def test_split_token_ranges_with_classes(eng, orc, rng, cuda):
     mask = tiled_mask(rng, T, T, 64)
     c = dit_case(orc, rng, T=T, Tq=T, B=1, H=8, mask=mask, ttype=F16)
     run_case(eng, orc, c, what="T=3000 tiled mask")
+
+
+def test_misaligned_workspace_rejected(eng, orc, rng, cuda):
+    """The class tables and split partials are written with aligned vector stores: a workspace
+    that is not 256-byte aligned is refused (CVATTN_ERR_BAD_ARGS) by single calls and by batch
+    preparation, before anything is launched; the aligned one runs."""
+    T = 700
+    c = dit_case(orc, rng, T=T, B=2, H=16, mask=tiled_mask(rng, T, T, 64), ttype=F16)
+    nws = eng.flash_attn_ext_workspace(c.q_d, c.k_d, c.v_d, c.mask_d)
+    assert nws > 0  # the class table at least
+    ws = workspace(nws + 256)
+    base = ws.data_ptr()
+    assert base % 256 == 0
+    rc = eng.flash_attn_ext(c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d, 0.125, base + 16, nws)
+    assert rc == cvattn.ERR_BAD_ARGS, eng.status_string(rc)
+    assert eng.flash_attn_ext(c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d, 0.125, base, nws) == cvattn.OK
+    p = cvattn.FaProblem()
+    p.q, p.k, p.v, p.mask, p.dst = c.q_d, c.k_d, c.v_d, c.mask_d, c.dst_d
+    nb = eng.fa_batch_workspace([p])
+    wb = workspace(nb + 256)
+    rc, _ = eng.fa_batch_prepare([p], 0.125, wb.data_ptr() + 64, nb)
+    assert rc == cvattn.ERR_BAD_ARGS, eng.status_string(rc)
+    torch.cuda.synchronize()
