@@ -321,7 +321,13 @@ void fa_rows_kernel(FaArgs args) {
                      : VTR   ? vt_d0 * (int)P.v_nb1 + 16 * vt_tc
                              : st_tok * nb1 + st_b * dblk_bytes<VT>();
 
-    RawBuf<W> R0, R1;
+    // Register buffers of staged tiles: tile t is loaded into R[t % NRB] NRB steps before the step
+    // that unpacks it into LDS (one step before the step that computes it).  The two-half f16
+    // form (prefill: one workgroup per CU, two waves per SIMD, so little else hides a load's
+    // latency) keeps three, 16 words each; the others keep two (a third cost the one-half
+    // forms 15-32 VGPRs: spills at the f16 cap, and 3 -> 2 waves per SIMD for q8_0).
+    constexpr int NRB = KT == T_F16 && VT == T_F16 && KH == 2 ? 3 : 2;
+    RawBuf<W> R[NRB];
     auto load_tile = [&](int t0, RawBuf<W> &r) {
         if (stage_k) {
             blk_load<KT>(rsrc, voff, t0 * nb1, r);
@@ -348,8 +354,8 @@ void fa_rows_kernel(FaArgs args) {
             blk_load<VT>(rsrc, voff, t0 * nb1, r);
         }
     };
-    load_tile(tok(0), R0);
-    load_tile(tok(1), R1);
+#pragma unroll
+    for (int j = 0; j < NRB; j++) load_tile(tok(j), R[j]);
 
     // ---- this lane's query rows (one per 16-row set) and their Q operands ----
     int row[NR], iq[NR], hq[NR];
@@ -842,8 +848,8 @@ void fa_rows_kernel(FaArgs args) {
     //      in pb across the barrier), then QK and softmax of tile s (K buffer s&1), while tile
     //      s+1 is unpacked into K buffer (s+1)&1 and V buffer (s+1)%3 from registers loaded two
     //      steps earlier; no buffer is written in the step that reads it ----
-    if (nsteps > 0) write_tile(R0, 0, tok(0));
-    load_tile(tok(2), R0);
+    if (nsteps > 0) write_tile(R[0], 0, tok(0));
+    load_tile(tok(NRB), R[0]);
     __syncthreads();
     // full steps run in the loop; only the last step can be partial, and it runs after the loop
     // from the buffers the loop staged it into
@@ -862,22 +868,47 @@ void fa_rows_kernel(FaArgs args) {
     // stage zeros into buffers nothing reads), and the loop has no early exit: the tile loads
     // are then counted exactly on every path, so each write waits only for its own tile.
     int s0 = 0;
-    for (; s0 + 1 < nfull; s0 += 2) {
-        // even step: stage step s0+1 from R1
-        step_full(s0);
-        write_tile(R1, s0 + 1, tok(s0 + 1));
-        load_tile(tok(s0 + 3), R1);
-        __syncthreads();
-        // odd step: stage step s0+2 from R0
-        step_full(s0 + 1);
-        write_tile(R0, s0 + 2, tok(s0 + 2));
-        load_tile(tok(s0 + 4), R0);
-        __syncthreads();
+    if constexpr (NRB == 2) {
+        for (; s0 + 1 < nfull; s0 += 2) {
+            // even step: stage step s0+1 from R[1]
+            step_full(s0);
+            write_tile(R[1], s0 + 1, tok(s0 + 1));
+            load_tile(tok(s0 + 3), R[1]);
+            __syncthreads();
+            // odd step: stage step s0+2 from R[0]
+            step_full(s0 + 1);
+            write_tile(R[0], s0 + 2, tok(s0 + 2));
+            load_tile(tok(s0 + 4), R[0]);
+            __syncthreads();
+        }
     }
-    if (s0 < nfull) { // an odd count of full steps: the last one
-        step_full(s0);
-        write_tile(R1, s0 + 1, tok(s0 + 1));
-        __syncthreads();
+    for (; NRB > 2 && s0 + NRB <= nfull; s0 += NRB) { // NRB > 2
+        // NRB steps with compile-time buffer indexes: step s0+j stages tile s0+j+1 from its
+        // buffer, which then takes the loads of tile s0+j+1+NRB
+#pragma unroll
+        for (int j = 0; j < NRB; j++) {
+            step_full(s0 + j);
+            write_tile(R[(j + 1) % NRB], s0 + j + 1, tok(s0 + j + 1));
+            load_tile(tok(s0 + j + 1 + NRB), R[(j + 1) % NRB]);
+            __syncthreads();
+        }
+    }
+    // the last nfull % NRB full steps (s0 is a multiple of NRB, so the buffer indexes continue)
+    if constexpr (NRB == 2) {
+        if (s0 < nfull) { // an odd count of full steps: the last one
+            step_full(s0);
+            write_tile(R[1], s0 + 1, tok(s0 + 1));
+            __syncthreads();
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j + 1 < NRB; j++) {
+            if (s0 + j < nfull) { // uniform
+                step_full(s0 + j);
+                write_tile(R[(j + 1) % NRB], s0 + j + 1, tok(s0 + j + 1));
+                __syncthreads();
+            }
+        }
     }
     if (nfull < nsteps) {
         // the partial last step: with two key halves, a half's 64 tokens may be full, partial or
