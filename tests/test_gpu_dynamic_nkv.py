@@ -114,3 +114,24 @@ def test_row_tiled_problems_follow_the_device_length(eng, orc, cuda):
         assert eng.fa_batch_launch(plan) == cvattn.OK
         torch.cuda.synchronize()
         check_at(orc, [c], n, "row-tiled")
+
+
+def test_classified_mask_follows_the_device_length(eng, orc, cuda):
+    """A mask shared by every head with more row groups than CUs (the classified form: the
+    classification runs at each launch over the keys below the device length, whose last tile
+    may be partial), over f16 K/V of capacity 700."""
+    from test_gpu_mask_classes import tiled_mask
+    rng = np.random.default_rng(11)
+    T = 700
+    c = dit_case(orc, rng, T=T, B=2, H=16, mask=tiled_mask(rng, T, T, 64), ttype=F16)
+    probs = problems_of([c])
+    n_kv = torch.tensor([0], dtype=torch.int32, device="cuda:0")
+    ws = workspace(eng.fa_batch_workspace(probs))
+    rc, plan = eng.fa_batch_prepare_dynamic(probs, 0.125, n_kv.data_ptr(), 0, ws.data_ptr(), ws.numel())
+    assert rc == cvattn.OK
+    for n in (700, 333, 64, 129, 699):
+        n_kv.fill_(n)
+        c.dst.fill_(float("nan"))
+        assert eng.fa_batch_launch(plan) == cvattn.OK
+        torch.cuda.synchronize()
+        check_at(orc, [c], n, "classified mask")
