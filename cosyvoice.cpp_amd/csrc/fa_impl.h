@@ -996,7 +996,11 @@ void fa_rows_kernel(FaArgs args) {
                 const float inv = l_run[r] > 0.0f ? 1.0f / l_run[r] : U.empty_row;
                 float *o = P.dst + (((int64_t)bq * U.n_q + iq[r]) * U.H + hq[r]) * HEAD;
 #pragma unroll
-                for (int i = 0; i < 4; i++) *(f4 *)&o[16 * i + 4 * g] = oacc[r][i] * inv;
+                for (int i = 0; i < 4; i++) {
+                    // the output is read by the next operation, not by this launch: non-temporal
+                    // stores (a 32 MB store probe: 7.4 -> 6.1 us)
+                    __builtin_nontemporal_store(oacc[r][i] * inv, (f4 *)&o[16 * i + 4 * g]);
+                }
             } else {
                 const int64_t slot = slot0 + (int64_t)(row[r] - rg * ROWS_ROWS) * P.n_splits + split;
                 float *o = U.partials + slot * PART_STRIDE;
