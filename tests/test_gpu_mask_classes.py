@@ -128,3 +128,17 @@ def test_misaligned_workspace_rejected(eng, orc, rng, cuda):
     rc, _ = eng.fa_batch_prepare([p], 0.125, wb.data_ptr() + 64, nb)
     assert rc == cvattn.ERR_BAD_ARGS, eng.status_string(rc)
     torch.cuda.synchronize()
+
+
+def test_prepared_batch_with_ragged_lengths(eng, orc, rng, cuda):
+    """Two prefill problems with different key lengths in one prepared batch (more row groups
+    than CUs together, so classified): each has its own class table, located by its first block
+    in the launch; checked over two launches."""
+    a = llm_case(orc, rng, nq=1200, nkv=1300, kt=Q8_0, vt=Q8_0, max_seq=1300,
+                 mask=tiled_mask(rng, 1200, 1300, 9), qscale=0.5)
+    b = llm_case(orc, rng, nq=1200, nkv=2100, kt=Q8_0, vt=Q8_0, max_seq=2100,
+                 mask=tiled_mask(rng, 1200, 2100, 9), qscale=0.5)
+    batch_run(eng, [a, b])
+    for i, c in enumerate((a, b)):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, c.mask_h, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"ragged batch, problem {i}")
