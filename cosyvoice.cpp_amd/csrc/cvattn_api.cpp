@@ -166,7 +166,8 @@ void plan_splits(const FaShape &sh, int n_kv, int64_t work, int *n_splits, int *
         // (1024-token prefill: 16.7 us unsplit vs 21.8 / 24.4 us with 2 / 3 splits).
         const int min_split = 256;
         const int64_t base = std::max<int64_t>(1, work);
-        const int64_t slots = (sh.ks.kh == 2 ? 1 : kRowsPerCu) * cu_count(); // two halves: 1 per CU (90 KB LDS)
+        // two halves (90 KB LDS) and the wide form (12 waves): 1 per CU
+        const int64_t slots = (sh.ks.kh == 2 || sh.ks.rows_per_group > 64 ? 1 : kRowsPerCu) * cu_count();
         int want = 1;
         if (2 * base < slots) {
             want = (int)((slots + base - 1) / base);
@@ -352,6 +353,19 @@ constexpr int kCvtMinRowGroups = 4;
 
 int64_t view_rows(const cvattn_tensor *t) { return t->ne[1] * t->ne[2] * t->ne[3]; }
 
+// The wide row-tiled form: one 192-row workgroup per CU, whose 12 waves share each staged K/V
+// tile (a third of the staging per row of the 64-row form).  Taken for unmasked one-half launches
+// of fp16 K/V with no split whose 192-row groups still give every CU one: the DiT call (T=1500,
+// 2 x 16 heads: 256 groups) 37.7-38.0 -> 33.3-34.8 us.
+static void make_wide(FaShape &sh) {
+    fa_shape_wide(sh.ks);
+    sh.n_rowgroups = (sh.n_rows + sh.ks.rows_per_group - 1) / sh.ks.rows_per_group;
+}
+static int64_t wide_groups(FaShape sh) {
+    make_wide(sh);
+    return (int64_t)sh.B * sh.H_kv * sh.n_rowgroups;
+}
+
 // Two key halves per row-tiled workgroup when the row groups alone would leave CUs idle (one
 // 8-wave workgroup per CU then runs each row set's key range in two halves); not for the
 // transposed-V form, whose dim-major tile holds one 64-token step.
@@ -387,6 +401,9 @@ int plan_single(const cvattn_tensor *q, const cvattn_tensor *k, const cvattn_ten
         bytes += (size_t)view_rows(v) * (size_t)pl->v_row * sizeof(_Float16);
     }
     // (the kernel sees the fp16 copies' type; the transposed-V form is not classified)
+    if (!vt && !sh.ks.wsplit && sh.ks.kh == 1 && pl->n_splits == 1 && !(mask && mask->data) &&
+        rows_wide_ok(pl->cvt_k ? T_F16 : k->type, pl->cvt_v ? T_F16 : v->type) && wide_groups(sh) >= cu_count())
+        make_wide(pl->sh);
     pl->mcls_ld = vt ? 0 : mcls_tiles(sh, mask, pl->cvt_k ? T_F16 : k->type, pl->cvt_v ? T_F16 : v->type);
     pl->mcls_off = 0;
     if (pl->mcls_ld) {
@@ -618,6 +635,18 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
     }
     if (table) table->resize(n);
     choose_kh(*sh0, work, false);
+    // the wide form (make_wide) when the launch's 192-row groups give every CU one
+    bool wide = !sh0->ks.wsplit && sh0->ks.kh == 1 && !has_mask && rows_wide_ok(probs[0].k.type, probs[0].v.type);
+    if (wide) {
+        int64_t g = 0;
+        for (int i = 0; i < n; i++) {
+            FaShape sh;
+            check_fa(&probs[i].q, &probs[i].k, &probs[i].v, nullptr, &sh);
+            g += wide_groups(sh);
+        }
+        wide = g >= cu_count();
+        if (wide) make_wide(*sh0);
+    }
     // decode: a second merge round only if all workgroups of the launch stay resident
     bool two_rounds = true;
     if (sh0->ks.wsplit) {
@@ -638,8 +667,12 @@ static int plan_batch(const cvattn_fa_problem *probs, int n, std::vector<FaProbl
         FaShape sh;
         check_fa(&p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &sh);
         sh.ks.kh = sh0->ks.kh;
+        if (wide) make_wide(sh);
         int ns, sl;
         plan_splits(sh, sh.n_kv, work, &ns, &sl, two_rounds);
+        // (the wide form never splits: its launches have more 64-row groups than CUs, so the
+        // planner's slots, one workgroup per CU, are never half idle)
+        if (wide && ns != 1) return CVATTN_ERR_UNSUPPORTED;
         FaProblem fp;
         fill_problem(fp, &p.q, &p.k, &p.v, has_mask ? &p.mask : nullptr, &p.dst, sh);
         fp.n_splits = ns;

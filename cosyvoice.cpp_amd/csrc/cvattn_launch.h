@@ -25,6 +25,10 @@ hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bo
                      hipStream_t st);
 // A row-tiled instance for classified mask tiles exists for this K/V type pair.
 bool rows_cls_ok(int ktype, int vtype);
+// The wide row-tiled form (12 waves, 192 rows per workgroup; unmasked, one key half) exists for
+// this K/V type pair; fa_shape_wide turns a row-tiled shape into it.
+bool rows_wide_ok(int ktype, int vtype);
+void fa_shape_wide(FaKernelShape &s);
 // Row-tiled attention over a transposed V (vtype T_VT_F32 / T_VT_F16), single calls.
 hipError_t fa_launch_vt(int ktype, int vtype, bool mask, const FaArgs &a, hipStream_t st);
 

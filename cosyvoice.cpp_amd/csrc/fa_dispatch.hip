@@ -10,6 +10,7 @@ FaLaunchFn fa_pick_rows(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_kh2(int mask, int batch, int ki, int vi);
 FaLaunchFn fa_pick_rows_vt(int mask, int ki, int vti);
 FaLaunchFn fa_pick_rows_cls(int batch, int ktype, int vtype);
+FaLaunchFn fa_pick_rows_wide(int batch, int ktype, int vtype);
 
 bool rows_cls_ok(int ktype, int vtype) { return fa_pick_rows_cls(0, ktype, vtype) != nullptr; }
 
@@ -44,6 +45,10 @@ FaKernelShape fa_shape(int n_rows, bool decode_ok) {
 
 hipError_t fa_launch(const FaKernelShape &s, int ktype, int vtype, bool mask, bool batch, const FaArgs &a,
                      hipStream_t st) {
+    if (!s.wsplit && s.nw == ROWS_NW_WIDE) {
+        const FaLaunchFn fn = mask || s.kh != 1 ? nullptr : fa_pick_rows_wide(batch, ktype, vtype);
+        return fn ? fn(a, st) : hipErrorInvalidValue;
+    }
     if (mask && !s.wsplit && s.kh == 1 && a.u.mcls_blocks > 0) {
         const FaLaunchFn fn = fa_pick_rows_cls(batch, ktype, vtype);
         return fn ? fn(a, st) : hipErrorInvalidValue;

@@ -43,6 +43,9 @@
 namespace cvattn {
 
 constexpr int ROWS_NW = 4;          // waves per workgroup
+// the wide form: 12 waves (192 rows) per workgroup, one workgroup per CU at 3 waves per SIMD, so
+// each staged K/V tile serves 192 rows (unmasked fp16 launches with a row group for every CU)
+constexpr int ROWS_NW_WIDE = 12;
 constexpr int ROWS_SETS = 1;        // 16-row sets per wave (a set shares every K and V operand read);
                                     // one set: 64-row workgroups, 3 resident per CU (138 VGPRs), measured
                                     // faster than two sets (128-row workgroups, 2 per CU) for prefill and DiT
@@ -208,8 +211,8 @@ __device__ __forceinline__ void merge_splits(const FaUniform &U, const FaProblem
 // take the first and second 64 tokens of each 128-token staged step, then merge through LDS.  For
 // launches with fewer row groups than CUs (prefill), where one wave per SIMD walks the whole key
 // range, this halves the chain each wave runs.
-template <int KT, int VT, int MASK, bool BATCH, int KH>
-__global__ __launch_bounds__(64 * ROWS_NW * KH)
+template <int KT, int VT, int MASK, bool BATCH, int KH, int NW>
+__global__ __launch_bounds__(64 * NW * KH)
 // f16 K/V without mask: 3 waves per SIMD (168 VGPRs).  The masked instance does not fit 168 (it
 // spilled 104-108 bytes per lane there) and runs faster unconstrained (DiT T=1500 with a 50-frame
 // chunk mask: 73.3 -> 71.0 us).
@@ -220,6 +223,9 @@ __attribute__((amdgpu_waves_per_eu(KH == 1 && KT == T_F16 && VT == T_F16 && MASK
 void fa_rows_kernel(FaArgs args) {
     constexpr int TS = ROWS_TS, NTILE = TS / 16, NKB = TS / 32, NR = ROWS_SETS;
     constexpr int TSS = TS * KH; // tokens per staged step
+    constexpr int ROWS = 16 * NR * NW; // rows per workgroup (row group)
+    static_assert(NW == ROWS_NW || (NW == ROWS_NW_WIDE && KH == 1 && MASK == 0 && !is_vt(VT)),
+                  "the wide form is one key half without mask");
     constexpr int RSK = ROWS_RS, RSV = is_vt(VT) ? ROWS_RS_VT : ROWS_RS;
     static_assert(KH == 1 || (KH == 2 && !is_vt(VT)), "the transposed-V tile holds one 64-token step");
     constexpr int W = blk_words<KT>() > blk_words<VT>() ? blk_words<KT>() : blk_words<VT>();
@@ -245,8 +251,8 @@ void fa_rows_kernel(FaArgs args) {
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int col = lane & 15; // MFMA column (query row) / A-operand row (token or dim)
     const int g = lane >> 4;   // lane group: k-slots 8g..8g+7, C rows 4g..4g+3
-    const int rw = wv & (ROWS_NW - 1);  // row wave: rows rw*16*NR.. of the row group
-    const int hk = KH == 2 ? wv >> 2 : 0; // key half (uniform per wave)
+    const int rw = wv % NW;               // row wave: rows rw*16*NR.. of the row group
+    const int hk = KH == 2 ? wv / NW : 0; // key half (uniform per wave)
 
     const int t_begin = split * P.split_len;
     const int t_end = min(P.n_kv, t_begin + P.split_len);
@@ -298,6 +304,9 @@ void fa_rows_kernel(FaArgs args) {
     constexpr int VDSTEP = 128 * KH / VCPD;       // dims between one thread's runs
     constexpr int VNCH = HEAD / VDSTEP;           // runs per staging thread
     const bool stage_k = wv < 2 * KH; // uniform per wave
+    // waves 0..4KH-1 stage the tiles; in the wide form the others only compute (their loads
+    // get an empty range: no memory traffic, and the wait counts stay those of the stagers)
+    const bool stager = NW == ROWS_NW || wv < 4 * KH;
     const int st_idx = tid & (128 * KH - 1);
     const int st_tok = st_idx >> 1, st_b = tid & 1;
     const int vt_tc = st_idx % VCPD, vt_d0 = st_idx / VCPD;
@@ -315,7 +324,7 @@ void fa_rows_kernel(FaArgs args) {
                          : VTR    ? (int64_t)(HEAD - 1) * P.v_nb1 + (int64_t)P.n_kv * VES + (VES == 2 ? 2 : 0)
                          : t_lim > 0 ? (int64_t)(t_lim - 1) * P.v_nb1 + 2 * dblk_bytes<VT>()
                                      : 0;
-    const __amdgpu_buffer_rsrc_t rsrc = stage_k ? make_rsrc(kbase, kext) : make_rsrc(vbase, vext);
+    const __amdgpu_buffer_rsrc_t rsrc = stage_k ? make_rsrc(kbase, kext) : make_rsrc(vbase, stager ? vext : 0);
     const int nb1 = stage_k ? (int)P.k_nb1 : VTR ? VES : (int)P.v_nb1; // bytes per token
     const int voff = stage_k ? st_tok * nb1 + st_b * dblk_bytes<KT>()
                      : VTR   ? vt_d0 * (int)P.v_nb1 + 16 * vt_tc
@@ -369,7 +378,7 @@ void fa_rows_kernel(FaArgs args) {
     bool row_ok[NR];
 #pragma unroll
     for (int r = 0; r < NR; r++) {
-        row[r] = rg * ROWS_ROWS + rw * (16 * NR) + 16 * r + col;
+        row[r] = rg * ROWS + rw * (16 * NR) + 16 * r + col;
         row_ok[r] = row[r] < U.n_rows;
         iq[r] = row_ok[r] ? row[r] / U.G : 0;
         hq[r] = kh * U.G + (row_ok[r] ? row[r] % U.G : 0);
@@ -412,7 +421,7 @@ void fa_rows_kernel(FaArgs args) {
         // beside Q (the loop then reads no memory for them)
         if constexpr (MASK == 2) {
             uint64_t pre = cls_pre; // uniform
-            const int q0 = rg * ROWS_ROWS / U.G;
+            const int q0 = rg * ROWS / U.G;
 #pragma unroll
             for (int i = 0; i < BND_HELD; i++) {
                 if (pre == 0) break; // uniform
@@ -479,6 +488,7 @@ void fa_rows_kernel(FaArgs args) {
     // unpack a staged tile's blocks (tokens t0..t0+TS) into LDS buffer `buf`
     // (step: the step of the tile: K buffer step&1, V buffer step%NVB)
     auto write_tile = [&](const RawBuf<W> &r, int step, int t0) {
+        if (!stager) return; // uniform
         float d, m;
         const int buf = step & 1, vbuf = step % NVB;
         if (stage_k) {
@@ -665,7 +675,7 @@ void fa_rows_kernel(FaArgs args) {
                     for (int r = 0; r < NR; r++) bnd[r] = (bnd_pk[r] >> (8 * idx)) & 0xff;
                 } else {
                     __builtin_amdgcn_sched_barrier(0);
-                    const int q0 = rg * ROWS_ROWS / U.G;
+                    const int q0 = rg * ROWS / U.G;
                     gu8 *b = gptr(mcls_bounds(P, U.mcls_blocks, (int64_t)rg * P.mcls_ld + kt0 + k));
 #pragma unroll
                     for (int r = 0; r < NR; r++) {
@@ -990,7 +1000,7 @@ void fa_rows_kernel(FaArgs args) {
 
     // ---------------- epilogue ----------------
     // partial slot of (row r of this row group, split s) = slot0 + r * n_splits + s
-    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * ROWS_ROWS * P.n_splits;
+    const int64_t slot0 = P.part_begin + (((int64_t)bq * U.H_kv + kh) * U.n_rowgroups + rg) * ROWS * P.n_splits;
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         l_run[r] = wave_sum16x4(l_run[r]);
@@ -1012,7 +1022,7 @@ void fa_rows_kernel(FaArgs args) {
                     __builtin_nontemporal_store(oacc[r][i] * inv, (f4 *)&o[16 * i + 4 * g]);
                 }
             } else {
-                const int64_t slot = slot0 + (int64_t)(row[r] - rg * ROWS_ROWS) * P.n_splits + split;
+                const int64_t slot = slot0 + (int64_t)(row[r] - rg * ROWS) * P.n_splits + split;
                 float *o = U.partials + slot * PART_STRIDE;
                 if constexpr (BATCH) {
                     // agent-coherent (sc1) vector stores, the form of agent-scope atomic stores
@@ -1050,7 +1060,7 @@ void fa_rows_kernel(FaArgs args) {
                 s_last = last ? 1u : 0u;
             }
             __syncthreads();
-            if (s_last) merge_splits<ROWS_ROWS, 64 * ROWS_NW * KH>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
+            if (s_last) merge_splits<ROWS, 64 * NW * KH>(U, P, bq, kh, rg, slot0, tid, (float *)&sK[0][0]);
         }
     }
 }
@@ -1096,16 +1106,16 @@ __global__ __launch_bounds__(64) void fa_combine_kernel(FaArgs args) {
 
 using FaLaunchFn = hipError_t (*)(const FaArgs &, hipStream_t);
 
-template <int KT, int VT, int MASK, bool BATCH, int KH = 1>
+template <int KT, int VT, int MASK, bool BATCH, int KH = 1, int NW = ROWS_NW>
 hipError_t launch_rows(const FaArgs &a, hipStream_t st) {
     if (a.u.total_units <= 0) return hipSuccess;
-    hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH, KH>), dim3((unsigned)a.u.total_units),
-                       dim3(64 * ROWS_NW * KH), 0, st, a);
+    hipLaunchKernelGGL((fa_rows_kernel<KT, VT, MASK, BATCH, KH, NW>), dim3((unsigned)a.u.total_units),
+                       dim3(64 * NW * KH), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // single calls merge split partials with a second launch; prepared batches merge in-kernel
     if (!BATCH && a.p0.n_splits > 1 && a.u.total_rows > 0) {
-        hipLaunchKernelGGL((fa_combine_kernel<ROWS_ROWS, BATCH>), dim3((unsigned)a.u.total_rows), dim3(64), 0, st, a);
+        hipLaunchKernelGGL((fa_combine_kernel<16 * ROWS_SETS * NW, BATCH>), dim3((unsigned)a.u.total_rows), dim3(64), 0, st, a);
         e = hipGetLastError();
     }
     return e;

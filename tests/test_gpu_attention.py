@@ -554,13 +554,28 @@ def batch_of(eng, cases, launches=1):
 
 def test_dit_t1500_f16_prepared_batch(eng, orc, cuda):
     """The benchmark's DiT call: f16 q/k/v views, T=1500, batch 2, 16 heads, no mask, through a
-    prepared batch (the timed form).  768 row groups > the CU count: one key half per workgroup."""
+    prepared batch (the timed form).  768 64-row groups > the CU count, and 256 192-row groups
+    (the last one 156 rows) give every CU one: the wide form (12 waves per workgroup)."""
     assert row_groups(2, 16, 1500) > cu_count()
+    assert row_groups(2, 16, 1500, 192) >= cu_count()
     rng = np.random.default_rng(1500)
     c = dit_case(orc, rng, T=1500, ttype=F16)
     batch_of(eng, [c], launches=2)
     want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
     check_close(host(c.dst), want, what="dit T=1500 f16 batch")
+
+
+def test_dit_wide_batch_ragged_lengths(eng, orc, cuda):
+    """The wide form over a prepared batch of two problems with different key lengths: 1200 f16
+    query rows per (batch, head) over 1200 and 700 keys (448 192-row groups, the last of each
+    head 48 rows), launched twice."""
+    assert row_groups(2, 16, 1200, 192) * 2 >= cu_count()
+    rng = np.random.default_rng(1200)
+    cases = [dit_case(orc, rng, T=nkv, Tq=1200, ttype=F16) for nkv in (1200, 700)]
+    batch_of(eng, cases, launches=2)
+    for c, nkv in zip(cases, (1200, 700)):
+        want = orc.fa_f64(c.q_h, c.k_h, c.v_h, None, 0.125, c.out_shape)
+        check_close(host(c.dst), want, what=f"dit wide batch, n_kv {nkv}")
 
 
 def dit_chunk_bounds(T, chunk=50):
