@@ -250,10 +250,12 @@ def test_dit_f16_inputs(eng, orc, rng, cuda):
     run_case(eng, orc, c, what="dit f16")
 
 
+@pytest.mark.parametrize("T", [400, 1500])
 @pytest.mark.parametrize("kt,vt", [(F32, F16), (F16, F32)])
-def test_dit_one_fp32_side(eng, orc, rng, kt, vt, cuda):
-    """Only one of K/V fp32: that side alone is copied to fp16 before the kernel runs."""
-    T, B, H = 400, 2, 16
+def test_dit_one_fp32_side(eng, orc, rng, kt, vt, T, cuda):
+    """Only one of K/V fp32: that side alone is copied to fp16 before the kernel runs (at T=1500
+    the kernel is the wide form: 192-row workgroups)."""
+    B, H = 2, 16
     c = Case()
     for name, t, n in (("q", F32, T), ("k", kt, T), ("v", vt, T)):
         x = rng.standard_normal((B, n, H * D)).astype(np.float32)
@@ -264,7 +266,7 @@ def test_dit_one_fp32_side(eng, orc, rng, kt, vt, cuda):
     c.out_shape = (B, T, H, D)
     c.dst = empty_f32(*c.out_shape)
     c.dst_d = cvattn.out_view(c.dst.data_ptr(), D, H, T, B)
-    run_case(eng, orc, c, what=f"dit k{kt} v{vt}")
+    run_case(eng, orc, c, what=f"dit T={T} k{kt} v{vt}")
 
 
 def test_dit_fp32_head_major_k_view(eng, orc, rng, cuda):
