@@ -106,6 +106,10 @@ TIMED_REPEATS = 25
 # untimed DiT calls before a DiT leg is timed: on MI355X the T=1500 call settles from ~35 us to
 # ~31 us over its first few hundred back-to-back calls (an utterance makes 220 of them)
 DIT_WARMUP_CALLS = 1000
+# untimed graph replays before the prefill, DiT-stream and serving legs (tens of milliseconds of
+# load, for the same clock settling), and before the layer-sequential decode cadence
+SETTLE_REPLAYS = 100
+CADENCE_SETTLE_REPLAYS = 10
 
 
 def time_graphs(torch, launch_fns, n_per_graph, warmup_steps, repeats=TIMED_REPEATS):
@@ -155,7 +159,7 @@ def decode_cadence(lib, cvattn, torch, dev, problem, n_copies, keep):
             for p in layer_plans[r]:
                 assert lib.fa_batch_launch(p, s) == cvattn.OK
 
-    ms_seq = time_graph(torch, launch_layers, n_copies, n_copies)
+    ms_seq = time_graph(torch, launch_layers, n_copies, CADENCE_SETTLE_REPLAYS * n_copies)
     log(f"decode 24 sequential layer launches: {ms_seq * 1e3:.2f} us/token")
 
     n_kv_dev = torch.full((n_copies,), NKV - 64, dtype=torch.int32, device=dev)
@@ -334,8 +338,8 @@ def bench_prefill(lib, cvattn, torch, dev):
         for pl in chunk_plans:
             assert lib.fa_batch_launch(pl, s) == cvattn.OK
 
-    ms = time_graph(torch, launch, L, L)
-    ms_chunks = time_graph(torch, launch_chunks, L, L)  # ms per layer (4 launches)
+    ms = time_graph(torch, launch, L, SETTLE_REPLAYS * L)
+    ms_chunks = time_graph(torch, launch_chunks, L, SETTLE_REPLAYS * L)  # ms per layer (4 launches)
     visible = sum(nkv - nq + ii + 1 for ii in range(nq))
     flops = 4.0 * D * H * visible
     # stored bytes per call: Q f32, K and V f16, O f32, the f16 mask
@@ -374,7 +378,7 @@ def bench_dit_stream(lib, cvattn, torch, dev):
         for pl in plans:
             assert lib.fa_batch_launch(pl, s) == cvattn.OK
 
-    ms = time_graph(torch, launch, NL, NL)
+    ms = time_graph(torch, launch, NL, SETTLE_REPLAYS * NL)
     nbytes = 2 * B * nkv * HD * D * 2 + 2 * B * nq * HD * D * 4
     return {"workload": "flow-DiT streaming call, 50-frame chunk over 1000 cached + 50 frames, batch 2, 16 heads, f16 cache",
             "us_per_layer_call": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9,
@@ -419,7 +423,7 @@ def bench_serving(lib, cvattn, torch, dev):
         for pl in plans:
             assert lib.fa_batch_launch(pl, s) == cvattn.OK
 
-    ms = time_graph(torch, launch, L, L)
+    ms = time_graph(torch, launch, L, SETTLE_REPLAYS * L)
     step_ms = ms * L
     return {"workload": "serving decode, 16 sequences x 24 layers, q8_0 K and V, ragged kv_len U{256..8192}, "
                         "one launch per layer", "kv_lens": [int(x) for x in lens],
